@@ -1,0 +1,241 @@
+"""Decode-step benchmark of the EntmaxKV MI355X build.
+
+Workload (BASELINE metric): B=8, H=32 (MHA), D=128, 32768-token prefill plus one
+appended token, page size 16, fp16, alpha=1.5.  One step = one call of
+``sparse_attention_decode_paged`` (token budget 1024, niter 2, the cache
+already appended, as in the reference's tests/run_benchmarks.py), with every
+input resident in HBM.  The Gaussian-aware step (tau_mode "corrected") on the
+same shape is reported alongside.
+
+value = effective bytes per step / step time, where the effective bytes are
+the selected K and V rows, one criticality bound per (b, h, page, d), q and
+out (the reference's accounting of the bytes a step must touch).
+
+Prints one JSON line.  --gpus N > 1 is rejected: this build measures one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def _args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--batch", type=int, default=8)
+    p.add_argument("--heads", type=int, default=32)
+    p.add_argument("--kv-heads", type=int, default=None)
+    p.add_argument("--head-dim", type=int, default=128)
+    p.add_argument("--kv-len", type=int, default=32768)
+    p.add_argument("--budget", type=int, default=1024)
+    p.add_argument("--niter", type=int, default=2)
+    p.add_argument("--alpha", type=float, default=1.5)
+    p.add_argument("--dtype", default="fp16", choices=["fp16", "bf16", "fp32"])
+    p.add_argument("--no-graph", action="store_true", help="time eager launches only")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-gaussian", action="store_true")
+    p.add_argument("--only", choices=["topk", "gaussian", "criticality"], default=None,
+                   help="run one step kind in a loop (for profilers)")
+    return p.parse_args()
+
+
+def _time_loop(fn, steps, warmup, stream):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms
+
+
+def _graphed(fn, stream):
+    import torch
+    g = torch.cuda.CUDAGraph()
+    fn()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g.replay
+
+
+def main():
+    a = _args()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
+                                   "(multi-GPU sharding is a design note, not built)"}))
+        return 2
+    import numpy as np
+    import torch
+
+    from entmaxkv_amd import (PagedKVCache, sparse_attention_decode_gaussian_aware_entmax,
+                              sparse_attention_decode_paged)
+
+    dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[a.dtype]
+    esz = torch.tensor([], dtype=dt).element_size()
+    B, H, D, L, ps = a.batch, a.heads, a.head_dim, a.kv_len, 16
+    Hkv = a.kv_heads or H
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    k = torch.randn(B, Hkv, L, D, device=dev, dtype=dt)
+    v = torch.randn(B, Hkv, L, D, device=dev, dtype=dt)
+    q = torch.randn(B, H, 1, D, device=dev, dtype=dt)
+    k_new = torch.randn(B, Hkv, 1, D, device=dev, dtype=dt)
+    v_new = torch.randn(B, Hkv, 1, D, device=dev, dtype=dt)
+    cache = PagedKVCache(page_size=ps)
+    cache.initialize(k, v)
+    cache.append(k_new, v_new)
+    del k, v
+    torch.cuda.empty_cache()
+
+    S = L + 1
+    P = (S + ps - 1) // ps
+    n_sel = min(a.budget // ps, P - 1)
+    lps = S - (P - 1) * ps
+    n_tok = n_sel * ps + lps
+    cache_seqlens = torch.full((B,), n_tok, device=dev, dtype=torch.int32)
+    q_seqlens = torch.full((B,), S, device=dev, dtype=torch.int32)
+    out = torch.zeros_like(q)
+    stream = torch.cuda.current_stream(dev)
+
+    def topk_step():
+        sparse_attention_decode_paged(q, cache, k_new, v_new, out, a.budget, cache_seqlens,
+                                      q_seqlens, alpha=a.alpha, niter=a.niter, append_cache=False)
+
+    def crit_only():
+        cache.select_topk(q, n_sel)
+
+    # effective (algorithmic) bytes: selected K+V rows, one bound per (b,h,page,d), q, out
+    kv_bytes = B * Hkv * n_tok * D * esz * 2
+    crit_bytes = B * H * (P - 1) * D * esz if Hkv == H else B * Hkv * (P - 1) * D * esz * 2
+    io_bytes = 2 * B * H * D * esz
+    step_bytes = kv_bytes + crit_bytes + io_bytes
+
+    if a.only:
+        fn = {"topk": topk_step, "criticality": crit_only}.get(a.only)
+        if a.only == "gaussian":
+            def fn():
+                sparse_attention_decode_gaussian_aware_entmax(q, cache, k_new, v_new, out,
+                                                              alpha=a.alpha, tau_mode="corrected")
+        ms = _time_loop(fn, a.steps, a.warmup, stream)
+        print(json.dumps({"only": a.only, "ms_per_step": ms}), flush=True)
+        return 0
+
+    ms_eager = _time_loop(topk_step, a.steps, a.warmup, stream)
+    ms_graph = None
+    if not a.no_graph:
+        replay = _graphed(topk_step, stream)
+        ms_graph = _time_loop(replay, a.steps, a.warmup, stream)
+    ms = ms_graph if ms_graph is not None else ms_eager
+
+    # dominant kernel: criticality (+ fused top-k); average launch time over the timed loop
+    ms_crit = _time_loop(crit_only, a.steps, a.warmup, stream)
+    crit_alg = crit_bytes + B * H * (P - 1) * esz  # bounds read + scores written
+    crit_gbs = crit_alg / (ms_crit * 1e-3) / 1e9
+
+    gauss = None
+    if not a.no_gaussian:
+        def gauss_step():
+            sparse_attention_decode_gaussian_aware_entmax(q, cache, k_new, v_new, out,
+                                                          alpha=a.alpha, tau_mode="corrected")
+        gms_eager = _time_loop(gauss_step, a.steps, a.warmup, stream)
+        gms_graph = None
+        if not a.no_graph:
+            greplay = _graphed(gauss_step, stream)
+            gms_graph = _time_loop(greplay, a.steps, a.warmup, stream)
+        sel = cache.last_num_selected_per_head.double()
+        sel_tok = float(((sel - 1).clamp(min=0) * ps + lps).sum().item())
+        g_bytes = B * Hkv * (P - 1) * D * esz * 2 + sel_tok * D * esz * 2 + io_bytes
+        gms = gms_graph if gms_graph is not None else gms_eager
+        gauss = {"us_per_step": gms * 1e3, "us_eager": gms_eager * 1e3,
+                 "effective_GBs": g_bytes / (gms * 1e-3) / 1e9,
+                 "pct_hbm_peak": 100.0 * g_bytes / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                 "mean_selected_pages": float(sel.mean().item()),
+                 "bytes_per_step": g_bytes}
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        cpu = _cpu_baseline(a, esz)
+
+    value = step_bytes / (ms * 1e-3) / 1e9
+    line = {
+        "metric": "decode-step us + effective KV GB/s (% HBM peak), B=8 H=32 D=128 L=32k alpha=1.5",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_step": round(ms * 1e3, 2),
+        "us_per_step_eager": round(ms_eager * 1e3, 2),
+        "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"fp16": "f16", "bf16": "bf16", "fp32": "f32"}[a.dtype] + " storage, f32 accumulate",
+        "data": "synthetic N(0,1) q/k/v, torch.manual_seed(0)",
+        "config": {"workload": "top-k paged sparse-entmax decode step", "batch": B, "q_heads": H,
+                   "kv_heads": Hkv, "head_dim": D, "kv_len": S, "page_size": ps,
+                   "token_budget": a.budget, "selected_tokens_per_head": n_tok,
+                   "alpha": a.alpha, "niter": a.niter, "timing": "hipGraph replay" if ms_graph else "eager",
+                   "bytes_per_step": step_bytes},
+        "roofline": {"bound": "hbm", "kernel": "criticality_kernel (fused top-k)",
+                     "achieved": round(crit_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(crit_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_launch_us": round(ms_crit * 1e3, 2), "bytes_per_launch": crit_alg},
+        "gaussian": gauss,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def _cpu_baseline(a, esz):
+    """The oracle's top-k step on one batch element of the workload, on the host."""
+    import numpy as np
+
+    from oracle import entmaxkv_oracle as O
+
+    rng = np.random.default_rng(0)
+    H, D, L, ps = a.heads, a.head_dim, a.kv_len, 16
+    Hkv = a.kv_heads or H
+    S = L + 1
+    k = O.round_to(rng.standard_normal((1, Hkv, S, D)), a.dtype)
+    v = O.round_to(rng.standard_normal((1, Hkv, S, D)), a.dtype)
+    q = O.round_to(rng.standard_normal((1, H, D)), a.dtype)
+    t0 = time.perf_counter()
+    st = O.page_stats(k, ps, a.dtype)  # not timed as part of the step below
+    t1 = time.perf_counter()
+    O.topk_decode_step(q, k, v, st, a.budget, ps, a.alpha, a.niter, a.dtype)
+    t2 = time.perf_counter()
+    P = (S + ps - 1) // ps
+    n_sel = min(a.budget // ps, P - 1)
+    n_tok = n_sel * ps + (S - (P - 1) * ps)
+    bytes_ = Hkv * n_tok * D * esz * 2 + H * (P - 1) * D * esz + 2 * H * D * esz
+    return {"value": round(bytes_ / (t2 - t1) / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port", "sample": f"one batch element (B=1, H={H}, L={S}) of the workload, "
+                                      f"NumPy float64 oracle, {t2 - t1:.2f} s per step",
+            "us_per_step": round((t2 - t1) * 1e6, 1)}
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,258 @@
+// Shared device helpers for the EntmaxKV CDNA4 (gfx950) kernels.
+//
+// Conventions used by every kernel in this library:
+//   * wave64; a "row segment" is the group of LPR consecutive lanes that hold
+//     one D-long row, each lane owning VEC = 16 / sizeof(T) contiguous elements
+//     (one 16-byte global load).  LPR = D / VEC is a power of two <= 64.
+//   * arithmetic is fp32; storage types are fp32, fp16 or bf16.
+//   * cross-workgroup reductions use a per-item arrival counter: the last
+//     workgroup to arrive finishes the item and resets the counter to zero, so
+//     workspaces are zeroed once at allocation and stay valid across calls.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+namespace ekv {
+
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+// ---------------------------------------------------------------------------
+// storage types
+// ---------------------------------------------------------------------------
+
+struct bf16_t { uint16_t bits; };
+
+template <typename T> struct Cvt;
+
+template <> struct Cvt<float> {
+  static __device__ __forceinline__ float to_f(float x) { return x; }
+  static __device__ __forceinline__ float from_f(float x) { return x; }
+};
+
+template <> struct Cvt<_Float16> {
+  static __device__ __forceinline__ float to_f(_Float16 x) { return (float)x; }
+  static __device__ __forceinline__ _Float16 from_f(float x) { return (_Float16)x; }
+};
+
+template <> struct Cvt<bf16_t> {
+  static __device__ __forceinline__ float to_f(bf16_t x) {
+    return __uint_as_float(((uint32_t)x.bits) << 16);
+  }
+  // round to nearest even; NaN stays a quiet NaN
+  static __device__ __forceinline__ bf16_t from_f(float x) {
+    uint32_t u = __float_as_uint(x);
+    bf16_t r;
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+      r.bits = (uint16_t)((u >> 16) | 0x40u);
+    } else {
+      u += 0x7fffu + ((u >> 16) & 1u);
+      r.bits = (uint16_t)(u >> 16);
+    }
+    return r;
+  }
+};
+
+template <typename T> __device__ __forceinline__ float to_f(T x) { return Cvt<T>::to_f(x); }
+template <typename T> __device__ __forceinline__ T from_f(float x) { return Cvt<T>::from_f(x); }
+
+// One 16-byte vector of T, converted to fp32 lanes.
+template <typename T> struct Vec {
+  static constexpr int N = 16 / sizeof(T);
+  float v[N];
+  __device__ __forceinline__ void load(const T* p) {
+    uint4 raw = *reinterpret_cast<const uint4*>(p);
+    const T* e = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = to_f<T>(e[i]);
+  }
+  __device__ __forceinline__ void store(T* p) const {
+    uint4 raw;
+    T* e = reinterpret_cast<T*>(&raw);
+#pragma unroll
+    for (int i = 0; i < N; ++i) e[i] = from_f<T>(v[i]);
+    *reinterpret_cast<uint4*>(p) = raw;
+  }
+};
+
+template <typename T> struct VecRaw {
+  static constexpr int N = 16 / sizeof(T);
+  uint4 raw;
+  __device__ __forceinline__ void load(const T* p) { raw = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ float get(int i) const {
+    return to_f<T>(reinterpret_cast<const T*>(&raw)[i]);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// wave-level reductions (wave64)
+// ---------------------------------------------------------------------------
+
+// Sum over an aligned segment of L lanes (L a power of two <= 64); every lane
+// of the segment receives the result.
+template <int L> __device__ __forceinline__ float seg_sum(float x) {
+#pragma unroll
+  for (int o = L / 2; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) { return seg_sum<64>(x); }
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+
+__device__ __forceinline__ int wave_sum_i(int x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// Block-wide exclusive scan of one int per thread (blockDim.x <= 1024).
+// `scratch` must hold blockDim.x / 64 + 1 ints.  Returns the exclusive prefix;
+// *total receives the block sum.  Contains __syncthreads.
+__device__ __forceinline__ int block_excl_scan(int x, int* scratch, int* total) {
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int nw = (blockDim.x + 63) >> 6;
+  int inc = wave_incl_scan(x);
+  if (lane == 63) scratch[wid] = inc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int w = 0; w < nw; ++w) {
+      int c = scratch[w];
+      scratch[w] = run;
+      run += c;
+    }
+    scratch[nw] = run;
+  }
+  __syncthreads();
+  int res = scratch[wid] + inc - x;
+  *total = scratch[nw];
+  __syncthreads();
+  return res;
+}
+
+// Block-wide sum of a float (deterministic order).  `scratch` >= 16 floats.
+__device__ __forceinline__ float block_sum(float x, float* scratch) {
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int nw = (blockDim.x + 63) >> 6;
+  x = wave_sum(x);
+  if (lane == 0) scratch[wid] = x;
+  __syncthreads();
+  float r = 0.f;
+  for (int w = 0; w < nw; ++w) r += scratch[w];
+  __syncthreads();
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// cross-workgroup completion
+// ---------------------------------------------------------------------------
+
+// Called by every thread of a workgroup after it has written its results.
+// Returns true in exactly one workgroup per counter: the last of `total`
+// arrivals.  That workgroup resets the counter to zero and, after return, sees
+// the global writes of all other arrivals (agent-scope release/acquire).
+__device__ __forceinline__ bool last_arrival(int* counter, int total) {
+  __shared__ int s_last;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    int last = (prev == total - 1);
+    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  const bool last = s_last != 0;
+  if (last) __threadfence();
+  return last;
+}
+
+// Loads that must observe other workgroups' writes made in the same kernel.
+__device__ __forceinline__ float ld_acquire(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ld_acquire(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// fp32 helpers with an explicit rounding sequence (no contraction)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
+__device__ __forceinline__ float fma_rn(float a, float b, float c) { return __fmaf_rn(a, b, c); }
+
+}  // namespace ekv
+
+// ---------------------------------------------------------------------------
+// host-side error reporting shared by all entry points
+// ---------------------------------------------------------------------------
+
+#define EKV_OK 0
+#define EKV_ERR_ARG (-1)
+#define EKV_ERR_HIP (-2)
+
+namespace ekv {
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace ekv
+
+namespace ekv {
+
+// Runtime dtype code -> storage type T (passed as a value of type T).
+// head_dim -> lanes per row (LPR) as an integral_constant.
+template <typename T, typename F>
+inline int dispatch_lpr(int D, F&& f) {
+  constexpr int VEC = 16 / sizeof(T);
+  if (D % VEC) return set_error(EKV_ERR_ARG, "head_dim %d must be a multiple of %d", D, VEC);
+  switch (D / VEC) {
+    case 4: return f(std::integral_constant<int, 4>{});
+    case 8: return f(std::integral_constant<int, 8>{});
+    case 16: return f(std::integral_constant<int, 16>{});
+    case 32: return f(std::integral_constant<int, 32>{});
+    case 64: return f(std::integral_constant<int, 64>{});
+    default:
+      return set_error(EKV_ERR_ARG, "head_dim %d unsupported (D/%d must be 4..64, power of two)", D,
+                       VEC);
+  }
+}
+
+template <typename F>
+inline int dispatch_dtype(int dtype, F&& f) {
+  switch (dtype) {
+    case kF32: return f(float{});
+    case kF16: return f(_Float16{});
+    case kBF16: return f(bf16_t{});
+    default: return set_error(EKV_ERR_ARG, "unknown dtype code %d", dtype);
+  }
+}
+
+}  // namespace ekv
+
+#define EKV_REQUIRE(cond, ...)                                  \
+  do {                                                          \
+    if (!(cond)) return ::ekv::set_error(EKV_ERR_ARG, __VA_ARGS__); \
+  } while (0)

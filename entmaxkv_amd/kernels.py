@@ -1,0 +1,455 @@
+"""Launchers for the HIP kernels, one per reference kernel module.
+
+Each launcher validates shapes and dtypes on the host (raising the same
+exception types the reference raises: AssertionError for shape asserts,
+ValueError for bad parameters), then calls one entry point of the C ABI on
+the current HIP stream.  No launcher synchronises with the device.
+"""
+
+from __future__ import annotations
+
+import math
+from statistics import NormalDist
+
+import torch
+
+from ._lib import call, dtype_code, lib, ptr, require_gpu, stream_ptr
+
+MAX_SPLITS_CAP = 256
+TOKENS_PER_SPLIT = 128
+
+
+def _row_major_d(t: torch.Tensor, name: str) -> torch.Tensor:
+    """Return ``t`` with a unit stride on the last dim and 16-byte aligned rows."""
+    esz = t.element_size()
+    vec = 16 // esz
+    ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+          and all(s % vec == 0 for s in t.stride()[:-1]))
+    return t if ok else t.contiguous()
+
+
+def choose_splits(max_tokens: int) -> int:
+    """Workgroups per (b, kv head) for the decode kernels."""
+    return int(max(1, min(MAX_SPLITS_CAP, math.ceil(max_tokens / TOKENS_PER_SPLIT))))
+
+
+def qscale_for(alpha: float, head_dim: int, dtype: torch.dtype) -> float:
+    """(alpha-1)/sqrt(D) rounded to the storage dtype (kernels/adadecode_paged.py:79,97,605)."""
+    c = (alpha - 1.0) * (1.0 / math.sqrt(head_dim))
+    return float(torch.tensor(c, dtype=torch.float64).to(dtype).to(torch.float64))
+
+
+def page_quantile_z(quantile: float, page_size: int) -> float:
+    """Normal quantile of quantile**(1/ps), as kernels/selection_pack.py:238-239."""
+    return NormalDist().inv_cdf(quantile ** (1.0 / page_size))
+
+
+# ---------------------------------------------------------------------------
+# page statistics (kv_cache.py:40-116)
+# ---------------------------------------------------------------------------
+
+def page_stats(k: torch.Tensor, kmin, kmax, kmean, kstd, seq_len: int, page_size: int,
+               page_begin: int, page_end: int) -> None:
+    """Fill stats for pages [page_begin, page_end) from rows of k [B, Hkv, S_cap, D]."""
+    require_gpu(k, kmin)
+    B, Hkv, _, D = k.shape
+    call("ekv_page_stats", k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+         kmin.data_ptr(), kmax.data_ptr(), kmean.data_ptr(), kstd.data_ptr(),
+         kmin.stride(0), kmin.stride(1), kmin.stride(2), B, Hkv, D, seq_len, page_size,
+         page_begin, page_end, dtype_code(k.dtype), stream_ptr(k.device))
+
+
+def append_token(k_new, v_new, k, v, kmin, kmax, kmean, kstd, pos: int, page_size: int,
+                 pos_per_batch: torch.Tensor | None = None) -> None:
+    """Write row ``pos`` of K/V and recompute its page statistics, in place."""
+    require_gpu(k_new, v_new, k)
+    B, Hkv, _, D = k.shape
+    k_new = _row_major_d(k_new, "k_new")
+    v_new = _row_major_d(v_new, "v_new")
+    if k_new.stride() != v_new.stride():
+        v_new = v_new.contiguous()
+        k_new = k_new.contiguous()
+    call("ekv_append", k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_new.stride(1),
+         k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+         kmin.data_ptr(), kmax.data_ptr(), kmean.data_ptr(), kstd.data_ptr(),
+         kmin.stride(0), kmin.stride(1), kmin.stride(2), B, Hkv, D, pos,
+         ptr(pos_per_batch), page_size, dtype_code(k.dtype), stream_ptr(k.device))
+
+
+# ---------------------------------------------------------------------------
+# criticality + top-k (kernels/page_criticality.py, attention_topk.py:52-71)
+# ---------------------------------------------------------------------------
+
+def estimate_page_criticality(q, k_min, k_max, alibi_slopes=None, q_pos: int = 0,
+                              page_size: int = 16, seq_len: int = 0,
+                              exclude_last_page: bool = False, out: torch.Tensor | None = None,
+                              topk: tuple | None = None) -> torch.Tensor:
+    """Upper-bound page scores [B, H, P(-1)] in the query dtype.
+
+    Mirrors triton_estimate_page_criticality (kernels/page_criticality.py:107-187,
+    apply_scaling=False).  ``topk=(k, last_page, page_indices, counters)`` fuses
+    the top-k page table into the same launch.
+    """
+    require_gpu(q, k_min, k_max)
+    B, H, _, D = q.shape
+    _, Hkv, stored_pages, _ = k_min.shape
+    num_pages = stored_pages - int(exclude_last_page)
+    if num_pages < 0:
+        raise ValueError("cannot exclude the last page from an empty cache")
+    if out is None:
+        out = torch.empty(B, H, num_pages, device=q.device, dtype=q.dtype)
+    if num_pages == 0:
+        return out
+    if k_min.stride() != k_max.stride():
+        raise ValueError("k_min and k_max must share strides")
+    q3 = _row_major_d(q.reshape(B, H, D) if q.shape[2] == 1 else q[:, :, 0], "q")
+    slopes = None
+    if alibi_slopes is not None:
+        slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
+    k_sel, last_page, pidx, counters = (-1, -1, None, None) if topk is None else topk
+    call("ekv_page_criticality", q3.data_ptr(), q3.stride(0), q3.stride(1),
+         k_min.data_ptr(), k_max.data_ptr(), k_min.stride(0), k_min.stride(1), k_min.stride(2),
+         ptr(slopes), out.data_ptr(), B, H, Hkv, D, num_pages, page_size, seq_len, q_pos,
+         k_sel, last_page, ptr(pidx), 0 if pidx is None else pidx.stride(0),
+         0 if pidx is None else pidx.stride(1), ptr(counters), dtype_code(q.dtype),
+         stream_ptr(q.device))
+    return out
+
+
+def topk_pages(scores: torch.Tensor, k: int, num_kv_heads: int, last_page: int = -1,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """Top-k page table [B, Hkv, k (+1)] from scores [B, H, P] (ascending, ties to lower id)."""
+    require_gpu(scores)
+    B, H, P = scores.shape
+    if not 0 <= k <= P:
+        raise ValueError(f"k={k} out of range for {P} pages")
+    width = k + (1 if last_page >= 0 else 0)
+    if out is None:
+        out = torch.empty(B, num_kv_heads, max(width, 1), device=scores.device, dtype=torch.int32)
+    scores = scores.contiguous()
+    call("ekv_topk_pages", scores.data_ptr(), B, H, num_kv_heads, P, k, last_page,
+         out.data_ptr(), out.stride(0), out.stride(1), dtype_code(scores.dtype),
+         stream_ptr(scores.device))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# paged decode (kernels/adadecode_paged.py:567-762, adadecode_paged_gaussian_tau.py)
+# ---------------------------------------------------------------------------
+
+class DecodeWorkspace:
+    """Zero-initialised device workspace for one decode shape (counters return to 0)."""
+
+    def __init__(self, batch, nheads, num_kv_heads, dim, splits, max_tokens, device):
+        self.spec = (batch, nheads, num_kv_heads, dim, splits, max_tokens, torch.device(device))
+        nbytes = lib().ekv_decode_workspace_bytes(batch, nheads, num_kv_heads, dim, splits,
+                                                  max_tokens)
+        self.buf = torch.zeros(int(nbytes), dtype=torch.uint8, device=device)
+        self.taus = torch.zeros(batch, nheads, dtype=torch.float32, device=device)
+        self.splits = splits
+        self.max_tokens = max_tokens
+
+
+def _cache_seqlens_2d(cache_seqlens, batch, num_kv_heads):
+    if cache_seqlens.dtype != torch.int32:
+        cache_seqlens = cache_seqlens.to(torch.int32)
+    if cache_seqlens.dim() == 1:
+        cache_seqlens = cache_seqlens[:, None].expand(batch, num_kv_heads)
+    assert tuple(cache_seqlens.shape) == (batch, num_kv_heads), "cache_seqlens must be [B, H_kv]"
+    return cache_seqlens
+
+
+def paged_entmax_decode(q, k_cache, v_cache, out, cache_seqlens, page_indices, page_size,
+                        alpha, tau_mode: int, iters: int, tau: torch.Tensor | None,
+                        alibi_slopes=None, q_seqlens=None, workspace: DecodeWorkspace | None = None,
+                        kv_rows: int | None = None):
+    """Shared launcher of the exact-tau (tau_mode 0) and given-tau (1) decode."""
+    require_gpu(q, k_cache, v_cache, out, page_indices)
+    batch, nheads, q_len, dim = q.shape
+    num_kv_heads = k_cache.shape[1]
+    assert q_len == 1
+    assert page_indices.dtype == torch.int32
+    assert nheads % num_kv_heads == 0, "Query heads must be divisible by KV heads"
+    assert tuple(v_cache.shape[:2]) == (batch, num_kv_heads), "K/V cache head shapes must match"
+    assert page_indices.shape[0] == batch, "page_indices batch mismatch"
+    assert page_indices.shape[1] == num_kv_heads, "page_indices must be keyed by KV heads"
+    if k_cache.stride() != v_cache.stride():
+        raise ValueError("k_cache and v_cache must share strides")
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+        raise TypeError("q, k_cache and v_cache must share a dtype")
+    cache_seqlens = _cache_seqlens_2d(cache_seqlens, batch, num_kv_heads)
+    if page_indices.stride(2) != 1:
+        page_indices = page_indices.contiguous()
+    n_slots = page_indices.shape[2]
+    max_tokens = n_slots * page_size
+    if workspace is None:
+        workspace = DecodeWorkspace(batch, nheads, num_kv_heads, dim, choose_splits(max_tokens),
+                                    max_tokens, q.device)
+    elif workspace.spec[:4] != (batch, nheads, num_kv_heads, dim) or workspace.max_tokens < max_tokens:
+        raise ValueError(f"invalid paged workspace {workspace.spec} for shape "
+                         f"{(batch, nheads, num_kv_heads, dim, max_tokens)}")
+    if tau is None:
+        tau = workspace.taus
+    assert tuple(tau.shape) == (batch, nheads) and tau.dtype == torch.float32 and tau.is_contiguous(), \
+        "tau must be a contiguous float32 [B, H] tensor"
+    q3 = _row_major_d(q[:, :, 0], "q")
+    o3 = out[:, :, 0]
+    direct = o3.stride(-1) == 1 and o3.data_ptr() % 16 == 0
+    o_target = o3 if direct else torch.empty(batch, nheads, dim, device=q.device, dtype=q.dtype)
+    slopes = None
+    if alibi_slopes is not None:
+        slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
+    qsl = None
+    if q_seqlens is not None:
+        qsl = q_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
+    if kv_rows is None:
+        kv_rows = k_cache.shape[2]
+    call("ekv_paged_entmax_decode",
+         q3.data_ptr(), q3.stride(0), q3.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
+         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), kv_rows,
+         page_indices.data_ptr(), page_indices.stride(0), page_indices.stride(1), n_slots,
+         cache_seqlens.data_ptr(), cache_seqlens.stride(0), cache_seqlens.stride(1),
+         ptr(qsl), ptr(slopes), tau.data_ptr(), tau_mode, iters,
+         o_target.data_ptr(), o_target.stride(0), o_target.stride(1), float(alpha),
+         qscale_for(alpha, dim, q.dtype), page_size, batch, nheads, num_kv_heads, dim,
+         workspace.splits, workspace.max_tokens, workspace.buf.data_ptr(),
+         workspace.buf.numel(), dtype_code(q.dtype), stream_ptr(q.device))
+    if not direct:
+        o3.copy_(o_target)
+    return out
+
+
+def sparse_attention_decode_paged(q, k_cache, v_cache, out, cache_seqlens, page_indices,
+                                  page_size, alibi_slopes=None, is_causal=True, alpha=1.5,
+                                  niter=10, max_splits=32, bins=16, q_seqlens=None,
+                                  taus_out=None, workspace=None):
+    """Exact-tau paged decode; mirrors kernels/adadecode_paged.py:567-762.
+
+    ``max_splits`` is accepted for signature parity; the split count is chosen
+    from the page table width (or taken from ``workspace``).  ``bins`` must be 16.
+    """
+    if bins != 16:
+        raise ValueError("only 16 histogram bins are supported")
+    paged_entmax_decode(q, k_cache, v_cache, out, cache_seqlens, page_indices, page_size, alpha,
+                        0, niter, taus_out, alibi_slopes, q_seqlens, workspace)
+    return out
+
+
+def sparse_attention_decode_paged_gaussian_tau(q, k_cache, v_cache, out, cache_seqlens,
+                                               page_indices, page_size, tau, alibi_slopes=None,
+                                               alpha=1.5, max_splits=32, q_seqlens=None,
+                                               tau_correction_iters=0, workspace=None):
+    """Given-tau paged decode; mirrors kernels/adadecode_paged_gaussian_tau.py:192-331.
+
+    ``tau`` [B, H] float32 is updated in place with the corrected value.
+    """
+    batch, nheads = q.shape[:2]
+    assert tuple(tau.shape) == (batch, nheads), "tau must be [B, H]"
+    paged_entmax_decode(q, k_cache, v_cache, out, cache_seqlens, page_indices, page_size, alpha,
+                        1, tau_correction_iters, tau, alibi_slopes, q_seqlens, workspace)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Gaussian statistics, tau solvers, selection (gaussian_page_stats.py, tau_solver_gpu.py,
+# tau_mixture_solver_triton.py, selection_pack.py, tau_clamp.py)
+# ---------------------------------------------------------------------------
+
+class GaussianBuffers:
+    """Persistent outputs + zero-initialised workspace of the Gaussian stats launch."""
+
+    def __init__(self, batch, nheads, num_kv_heads, dim, pages, dtype, device):
+        f = dict(dtype=torch.float32, device=device)
+        self.spec = (batch, nheads, num_kv_heads, dim, pages, dtype, torch.device(device))
+        self.mu_p = torch.empty(batch, nheads, pages, **f)
+        self.sigma_p = torch.empty(batch, nheads, pages, **f)
+        self.mu_g = torch.empty(batch, nheads, 1, **f)
+        self.sigma_g = torch.empty(batch, nheads, 1, **f)
+        self.mean_var = torch.empty(batch, nheads, 1, **f)
+        self.var_means = torch.empty(batch, nheads, 1, **f)
+        self.tau_hat = torch.empty(batch, nheads, **f)
+        nbytes = lib().ekv_gaussian_workspace_bytes(batch, nheads, num_kv_heads, dim, pages,
+                                                    dtype_code(dtype))
+        self.ws = torch.zeros(int(nbytes), dtype=torch.uint8, device=device)
+
+
+def compute_page_gaussian_stats(q, k_mean, k_std, pages_for_stats, *, alibi_slopes=None,
+                                page_size=16, seq_len=0, alpha=1.5, n_tokens=None,
+                                solve_tau=True, tau_iters=120, tol=1e-6,
+                                buffers: GaussianBuffers | None = None) -> GaussianBuffers:
+    """Per-page score moments, global moments and (optionally) the fused tau-hat.
+
+    Mirrors compute_page_gaussian_stats_triton (kernels/gaussian_page_stats.py:128-233,
+    return_sigma=True) plus gaussian_utils.py:142-181.  ``n_tokens`` defaults to
+    pages_for_stats * page_size (seq_len_for_stats).
+    """
+    require_gpu(q, k_mean, k_std)
+    if q.shape[0] != k_mean.shape[0] or q.shape[1] % k_mean.shape[1] != 0:
+        raise ValueError("q and k_mean must have matching batch/head dimensions")
+    if k_mean.shape != k_std.shape or k_mean.stride() != k_std.stride():
+        raise ValueError("k_mean and k_std must have identical shapes")
+    if pages_for_stats <= 0:
+        raise ValueError("pages_for_stats must be positive")
+    if pages_for_stats > k_mean.shape[2]:
+        raise ValueError("pages_for_stats exceeds the available pages")
+    if q.shape[-1] != k_mean.shape[-1]:
+        raise ValueError("q and page statistics must have matching head dimensions")
+    B, H, _, D = q.shape
+    Hkv = k_mean.shape[1]
+    if buffers is None or buffers.spec != (B, H, Hkv, D, pages_for_stats, q.dtype, q.device):
+        buffers = GaussianBuffers(B, H, Hkv, D, pages_for_stats, q.dtype, q.device)
+    if n_tokens is None:
+        n_tokens = pages_for_stats * page_size
+    q3 = _row_major_d(q[:, :, 0], "q")
+    slopes = None
+    if alibi_slopes is not None:
+        slopes = alibi_slopes.to(device=q.device, dtype=torch.float32)
+        if slopes.dim() == 2:
+            slopes = slopes[0]
+        slopes = slopes.contiguous()
+    call("ekv_gaussian_page_stats", q3.data_ptr(), q3.stride(0), q3.stride(1),
+         k_mean.data_ptr(), k_std.data_ptr(), k_mean.stride(0), k_mean.stride(1),
+         k_mean.stride(2), pages_for_stats, ptr(slopes), page_size, seq_len,
+         buffers.mu_p.data_ptr(), buffers.sigma_p.data_ptr(), buffers.mu_g.data_ptr(),
+         buffers.sigma_g.data_ptr(), buffers.mean_var.data_ptr(), buffers.var_means.data_ptr(),
+         buffers.tau_hat.data_ptr() if solve_tau else None, float(alpha), int(n_tokens),
+         int(tau_iters), float(tol), B, H, Hkv, D, buffers.ws.data_ptr(), buffers.ws.numel(),
+         dtype_code(q.dtype), stream_ptr(q.device))
+    return buffers
+
+
+def solve_for_tau_hat_single_gaussian_gpu(mu_g, sigma_g, n, alpha, iterations=120, tol=1e-6,
+                                          out=None):
+    """One lane per (b, h) tau-hat; mirrors kernels/tau_solver_gpu.py:128-158."""
+    require_gpu(mu_g, sigma_g)
+    shape = mu_g.shape
+    mu = mu_g.contiguous().view(-1).to(torch.float32)
+    sg = sigma_g.contiguous().view(-1).to(torch.float32)
+    res = torch.empty_like(mu) if out is None else out.view(-1)
+    call("ekv_tau_single_gaussian", mu.data_ptr(), sg.data_ptr(), res.data_ptr(), mu.numel(),
+         int(n), float(alpha), int(iterations), float(tol), stream_ptr(mu.device))
+    return res.view(shape)
+
+
+def solve_for_tau_hat_page_gaussian_mixture(mu_pages, sigma_pages, page_counts=None, alpha=1.5,
+                                            max_iter=40, tol=1e-6, uniform_page_count=1.0):
+    """Page-mixture tau-hat [..., 1]; mirrors kernels/tau_mixture_solver_triton.py:172-240.
+
+    Per-page counts other than one uniform value are not supported by the
+    native kernel (the reference path only passes a uniform count,
+    gaussian_utils.py:171-177).
+    """
+    if mu_pages.shape != sigma_pages.shape:
+        raise ValueError(f"mu_pages and sigma_pages must have the same shape, got "
+                         f"{tuple(mu_pages.shape)} and {tuple(sigma_pages.shape)}")
+    if mu_pages.dim() < 1:
+        raise ValueError("mu_pages must have a page dimension")
+    if alpha not in (2, 1.5, 4 / 3):
+        raise ValueError(f"Unsupported alpha for page-mixture tau solve: {alpha}")
+    if page_counts is not None:
+        pc = torch.as_tensor(page_counts)
+        if pc.numel() != 1 and not bool((pc == pc.reshape(-1)[0]).all()):
+            raise ValueError("non-uniform page_counts are not supported")
+        uniform_page_count = float(pc.reshape(-1)[0])
+    if uniform_page_count <= 0:
+        raise ValueError("uniform_page_count must be positive")
+    require_gpu(mu_pages, sigma_pages)
+    pages = mu_pages.shape[-1]
+    if pages <= 0:
+        raise ValueError("mu_pages must have a non-empty page dimension")
+    rows = mu_pages.numel() // pages
+    mu = mu_pages.to(torch.float32).contiguous()
+    sg = sigma_pages.to(torch.float32).contiguous()
+    out = torch.empty(rows, device=mu.device, dtype=torch.float32)
+    call("ekv_tau_page_mixture", mu.data_ptr(), sg.data_ptr(), out.data_ptr(), rows, pages,
+         float(uniform_page_count), float(alpha), int(max_iter), float(tol), stream_ptr(mu.device))
+    return out.view(*mu_pages.shape[:-1], 1).to(mu_pages.dtype)
+
+
+def select_gaussian_threshold_pack(mu_p, sigma_p, tau_hat, sigma_g, page_size, alpha,
+                                   safety_margin_z, max_quantile,
+                                   threshold_excess_margin_fraction, pages_for_stats, num_pages,
+                                   num_kv_heads=None, out=None, counts=None, tau_floor=None,
+                                   cache_seqlens=None, last_page_size=None, tau_clamped=None,
+                                   clamp_quantile=0.5, eps=1e-4, effective=None):
+    """Threshold select + pack (+ fused lengths and tau clamp).
+
+    Mirrors select_gaussian_threshold_pack_triton (kernels/selection_pack.py:201-272).
+    ``safety_margin_z``/``max_quantile`` None selects the automatic margins of
+    gaussian_utils.py:163-169, computed on the device.
+    Returns (page_indices [B, Hkv, num_pages], counts [B, Hkv], tau_floor [B, H]).
+    """
+    require_gpu(mu_p, sigma_p, tau_hat, sigma_g)
+    if mu_p.dim() != 3:
+        raise ValueError("mu_scores_per_page must have shape [batch, heads, pages]")
+    if pages_for_stats <= 0 or num_pages <= 0:
+        raise ValueError("pages_for_stats and num_pages must be positive")
+    B, H, _ = mu_p.shape
+    Hkv = H if num_kv_heads is None else num_kv_heads
+    dev = mu_p.device
+    if out is None:
+        out = torch.empty(B, Hkv, num_pages, dtype=torch.int32, device=dev)
+    if counts is None:
+        counts = torch.empty(B, Hkv, dtype=torch.int32, device=dev)
+    if tau_floor is None:
+        tau_floor = torch.empty(B, H, dtype=torch.float32, device=dev)
+    th = tau_hat.reshape(B, H).to(torch.float32).contiguous()
+    sg = sigma_g.reshape(B, H).to(torch.float32).contiguous()
+    auto = safety_margin_z is None or max_quantile is None
+    z_low = page_quantile_z(0.99, page_size)
+    z_high = page_quantile_z(0.995, page_size)
+    z_page = page_quantile_z(max_quantile, page_size) if not auto else 0.0
+    smz = float(safety_margin_z) if not auto else 0.0
+    z_clamp = page_quantile_z(clamp_quantile, page_size)
+    if last_page_size is None:
+        last_page_size = page_size
+    call("ekv_select_gaussian_pack", mu_p.contiguous().data_ptr(), sigma_p.contiguous().data_ptr(),
+         th.data_ptr(), sg.data_ptr(), B, H, Hkv, pages_for_stats, num_pages, float(alpha),
+         int(auto), smz, z_page, z_low, z_high, float(threshold_excess_margin_fraction),
+         out.data_ptr(), out.stride(0), out.stride(1), counts.data_ptr(), tau_floor.data_ptr(),
+         ptr(cache_seqlens), page_size, last_page_size, ptr(tau_clamped), z_clamp, float(eps),
+         ptr(effective), stream_ptr(dev))
+    return out, counts, tau_floor
+
+
+def clamp_tau_to_selected_page_statistics(tau, mu_p, sigma_p, page_indices, num_selected,
+                                          tau_floor, page_size, alpha, clamp_quantile,
+                                          pages_for_stats, eps=1e-4):
+    """Standalone tau clamp; mirrors kernels/tau_clamp.py:76-151."""
+    require_gpu(tau, mu_p, sigma_p, page_indices, num_selected)
+    if pages_for_stats <= 0:
+        return tau.contiguous()
+    original_shape = tau.shape
+    t2 = tau.squeeze(-1) if tau.dim() == 3 and tau.shape[-1] == 1 else tau
+    B, H = t2.shape
+    t2 = t2.to(torch.float32).contiguous()
+    if page_indices.shape[-1] <= 0:
+        out = t2.clone()
+        return out.unsqueeze(-1) if original_shape != out.shape else out
+    Hsel = page_indices.shape[1]
+    pi = page_indices if page_indices.stride(-1) == 1 else page_indices.contiguous()
+    tf = None
+    if tau_floor is not None:
+        tf = tau_floor.squeeze(-1) if tau_floor.dim() == 3 and tau_floor.shape[-1] == 1 else tau_floor
+        tf = tf.to(device=t2.device, dtype=torch.float32).contiguous()
+    out = torch.empty_like(t2)
+    ns = num_selected.to(torch.int32)
+    call("ekv_tau_clamp", t2.data_ptr(), mu_p.contiguous().data_ptr(),
+         sigma_p.contiguous().data_ptr(), pi.data_ptr(), pi.stride(0), pi.stride(1),
+         pi.shape[-1], ns.data_ptr(), ns.stride(0), ns.stride(1), ptr(tf), out.data_ptr(), B, H,
+         Hsel, pages_for_stats, float(alpha), page_quantile_z(clamp_quantile, page_size),
+         float(eps), stream_ptr(t2.device))
+    if original_shape != out.shape:
+        out = out.unsqueeze(-1)
+    return out
+
+
+def cache_seqlens_from_page_counts(counts, page_size, last_page_size, out=None):
+    """max(count-1, 0)*ps + last_page_size; mirrors kernels/selection_pack.py:23-43."""
+    require_gpu(counts)
+    c = counts.to(torch.int32).contiguous()
+    if out is None:
+        out = torch.empty_like(c)
+    call("ekv_cache_seqlens_from_counts", c.data_ptr(), out.data_ptr(), c.numel(), page_size,
+         last_page_size, stream_ptr(c.device))
+    return out

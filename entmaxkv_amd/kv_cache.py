@@ -1,0 +1,308 @@
+"""Paged KV cache with per-page key statistics, MI355X layout.
+
+Drop-in for ``entmaxkv.kv_cache.PagedKVCache`` (kv_cache.py:16-255): same
+constructor, methods and attributes.  What changes is the storage:
+
+* K and V live in preallocated capacity buffers ``[B, Hkv, S_cap, D]``;
+  ``k_cache``/``v_cache`` are views of the first ``seq_len`` rows.  ``append``
+  writes one row in place (one kernel launch that also refreshes the last
+  page's statistics) instead of ``torch.cat`` of the whole cache
+  (kv_cache.py:81-82), and capacity grows geometrically when full.
+* The four statistics are interleaved per page: ``bounds [B, Hkv, P_cap, 2, D]``
+  holds (min, max) and ``moments [B, Hkv, P_cap, 2, D]`` holds (mean, std), so
+  the criticality kernel reads one contiguous 2*D run per page and the
+  Gaussian kernel another.  ``k_min``/``k_max``/``k_mean``/``k_std`` are views
+  ``[B, Hkv, P, D]`` of them.
+* ``initialize`` computes all page statistics with one kernel launch instead
+  of a Python loop over pages (kv_cache.py:58-70).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import kernels as K
+
+
+def _round_up(x: int, m: int) -> int:
+    return (x + m - 1) // m * m
+
+
+class PagedKVCache:
+    """KV cache with paged min/max/mean/std metadata (kv_cache.py:16-38)."""
+
+    def __init__(self, page_size: int = 16, capacity: Optional[int] = None,
+                 headroom: int = 1024):
+        self.page_size = page_size
+        self.capacity = capacity
+        self.headroom = headroom
+        self.seq_len = 0
+        self._k = None
+        self._v = None
+        self._bounds = None
+        self._moments = None
+
+        self.last_num_selected_per_head = None
+        self.last_effective_safety_margin = None
+        self.last_effective_max_quantile = None
+        self.last_page_scores = None
+
+        self._page_indices_buf: Optional[torch.Tensor] = None
+        self._page_indices_last_page: Optional[int] = None
+        self._topk_counters: Optional[torch.Tensor] = None
+        self._scores_buf: Optional[torch.Tensor] = None
+        self._paged_decode_workspaces: dict = {}
+        self._gaussian_buffers: dict = {}
+        self._select_buffers: dict = {}
+
+    # ------------------------------------------------------------------ views
+    @property
+    def num_pages(self) -> int:
+        return (self.seq_len + self.page_size - 1) // self.page_size
+
+    @property
+    def k_cache(self):
+        return None if self._k is None else self._k[:, :, : self.seq_len]
+
+    @property
+    def v_cache(self):
+        return None if self._v is None else self._v[:, :, : self.seq_len]
+
+    def _stat(self, buf, j):
+        return None if buf is None else buf[:, :, : self.num_pages, j]
+
+    @property
+    def k_min(self):
+        return self._stat(self._bounds, 0)
+
+    @property
+    def k_max(self):
+        return self._stat(self._bounds, 1)
+
+    @property
+    def k_mean(self):
+        return self._stat(self._moments, 0)
+
+    @property
+    def k_std(self):
+        return self._stat(self._moments, 1)
+
+    @property
+    def kv_capacity(self) -> int:
+        return 0 if self._k is None else self._k.shape[2]
+
+    # ------------------------------------------------------------- storage
+    def _allocate(self, batch, num_heads, cap, head_dim, dtype, device):
+        cap = _round_up(max(cap, self.page_size), self.page_size)
+        pcap = cap // self.page_size
+        k = torch.empty(batch, num_heads, cap, head_dim, dtype=dtype, device=device)
+        v = torch.empty_like(k)
+        bounds = torch.zeros(batch, num_heads, pcap, 2, head_dim, dtype=dtype, device=device)
+        moments = torch.zeros_like(bounds)
+        return k, v, bounds, moments
+
+    def _grow(self, needed: int):
+        B, H, cap, D = self._k.shape
+        new_cap = max(needed, 2 * cap)
+        k, v, bounds, moments = self._allocate(B, H, new_cap, D, self._k.dtype, self._k.device)
+        k[:, :, :cap].copy_(self._k)
+        v[:, :, :cap].copy_(self._v)
+        pc = self._bounds.shape[2]
+        bounds[:, :, :pc].copy_(self._bounds)
+        moments[:, :, :pc].copy_(self._moments)
+        self._k, self._v, self._bounds, self._moments = k, v, bounds, moments
+
+    def initialize(self, k: torch.Tensor, v: torch.Tensor):
+        """Initialize the cache with prefill keys/values (kv_cache.py:40-70)."""
+        if not k.is_cuda:
+            raise ValueError("PagedKVCache requires GPU tensors")
+        batch, num_heads, seq_len, head_dim = k.shape
+        cap = self.capacity if self.capacity is not None else seq_len + self.headroom
+        cap = max(cap, seq_len + 1)
+        self._k, self._v, self._bounds, self._moments = self._allocate(
+            batch, num_heads, cap, head_dim, k.dtype, k.device)
+        self._k[:, :, :seq_len].copy_(k)
+        self._v[:, :, :seq_len].copy_(v)
+        self.seq_len = seq_len
+        self._page_indices_buf = None
+        self._page_indices_last_page = None
+        if seq_len > 0:
+            K.page_stats(self._k, self._bounds[:, :, :, 0], self._bounds[:, :, :, 1],
+                         self._moments[:, :, :, 0], self._moments[:, :, :, 1], seq_len,
+                         self.page_size, 0, self.num_pages)
+
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor):
+        """Append one token per (b, kv head) and update its page's stats (kv_cache.py:72-116).
+
+        k_new, v_new: [batch, num_heads, 1, head_dim].
+        """
+        if k_new.shape[2] != 1:
+            for t in range(k_new.shape[2]):
+                self.append(k_new[:, :, t:t + 1], v_new[:, :, t:t + 1])
+            return
+        pos = self.seq_len
+        if pos + 1 > self.kv_capacity:
+            self._grow(pos + 1 + self.headroom)
+        K.append_token(k_new[:, :, 0], v_new[:, :, 0], self._k, self._v,
+                       self._bounds[:, :, :, 0], self._bounds[:, :, :, 1],
+                       self._moments[:, :, :, 0], self._moments[:, :, :, 1], pos, self.page_size)
+        self.seq_len = pos + 1
+
+    # ---------------------------------------------------------- criticality
+    def estimate_page_criticality(self, q: torch.Tensor, use_triton: bool = False,
+                                  alibi_slopes=None, q_pos: int = 0,
+                                  exclude_last_page: bool = False) -> torch.Tensor:
+        """Upper-bound page scores [B, H, pages] (kv_cache.py:118-165).
+
+        ``use_triton`` is accepted for compatibility; the native kernel always runs.
+        """
+        return K.estimate_page_criticality(
+            q, self.k_min, self.k_max, alibi_slopes=alibi_slopes, q_pos=q_pos,
+            page_size=self.page_size, seq_len=self.seq_len,
+            exclude_last_page=exclude_last_page)
+
+    def select_topk(self, q: torch.Tensor, k: int, alibi_slopes=None) -> torch.Tensor:
+        """Fused criticality + top-k page table [B, Hkv, k + 1] (last page at slot k).
+
+        Replaces attention_topk.py:45-71.  Under GQA a kv head's page score is
+        the maximum of its query heads' scores.
+        """
+        B, H = q.shape[:2]
+        Hkv = self._k.shape[1]
+        P = self.num_pages
+        last = P - 1
+        buf = self.get_page_indices_buf(B, Hkv, k, last)
+        scores = self._get_scores_buf(B, H, P - 1, q.dtype, q.device)
+        self.last_page_scores = scores
+        if k == 0:
+            return buf
+        if self._topk_counters is None or self._topk_counters.numel() < B * Hkv \
+                or self._topk_counters.device != q.device:
+            self._topk_counters = torch.zeros(B * Hkv, dtype=torch.int32, device=q.device)
+        K.estimate_page_criticality(
+            q, self.k_min, self.k_max, alibi_slopes=alibi_slopes, q_pos=self.seq_len - 1,
+            page_size=self.page_size, seq_len=self.seq_len, exclude_last_page=True,
+            out=scores, topk=(k, last, buf, self._topk_counters))
+        return buf
+
+    def _get_scores_buf(self, B, H, P, dtype, device):
+        buf = self._scores_buf
+        need = B * H * max(P, 1)
+        if buf is None or buf.numel() < need or buf.dtype != dtype or buf.device != device:
+            buf = torch.empty(max(need, 2 * need), dtype=dtype, device=device)
+            self._scores_buf = buf
+        return buf[: B * H * P].view(B, H, P)
+
+    # ---------------------------------------------------------- buffers
+    def get_page_indices_buf(self, batch: int, num_heads: int, num_pages_to_select: int,
+                             last_page_idx: int) -> torch.Tensor:
+        """Persistent [B, H, n_selected+1] page-index buffer (kv_cache.py:167-185).
+
+        The sentinel column is written by the selection kernel on every call, so
+        no per-step fill is needed; it is filled here only when nothing is
+        selected.
+        """
+        target_shape = (batch, num_heads, num_pages_to_select + 1)
+        buf = self._page_indices_buf
+        device = self._k.device
+        if buf is None or tuple(buf.shape) != target_shape or buf.device != device:
+            buf = torch.empty(target_shape, dtype=torch.int32, device=device)
+            self._page_indices_buf = buf
+            self._page_indices_last_page = None
+        if num_pages_to_select == 0 and self._page_indices_last_page != last_page_idx:
+            buf[:, :, 0].fill_(last_page_idx)
+        self._page_indices_last_page = last_page_idx
+        return buf
+
+    def get_paged_decode_workspace(self, batch: int, nheads: int, dim: int, max_splits: int,
+                                   bins: int, dtype: torch.dtype, device, *,
+                                   num_kv_heads: Optional[int] = None,
+                                   max_tokens: Optional[int] = None) -> K.DecodeWorkspace:
+        """Persistent decode workspace for one shape (kv_cache.py:187-203).
+
+        ``max_splits`` and ``bins`` are accepted for signature parity; the split
+        count follows from ``max_tokens`` (the page-table width times page size).
+        """
+        device = torch.device(device)
+        if num_kv_heads is None:
+            num_kv_heads = self._k.shape[1]
+        if max_tokens is None:
+            max_tokens = self.num_pages * self.page_size
+        splits = K.choose_splits(max_tokens)
+        key = (batch, nheads, num_kv_heads, dim, splits, max_tokens, device.type, device.index)
+        ws = self._paged_decode_workspaces.get(key)
+        if ws is None:
+            ws = K.DecodeWorkspace(batch, nheads, num_kv_heads, dim, splits, max_tokens, device)
+            self._paged_decode_workspaces[key] = ws
+        return ws
+
+    def get_gaussian_buffers(self, q: torch.Tensor, pages_for_stats: int) -> K.GaussianBuffers:
+        B, H, _, D = q.shape
+        key = (B, H, self._k.shape[1], D, pages_for_stats, q.dtype, q.device)
+        buf = self._gaussian_buffers.get(key)
+        if buf is None:
+            self._gaussian_buffers.clear()
+            buf = K.GaussianBuffers(B, H, self._k.shape[1], D, pages_for_stats, q.dtype, q.device)
+            self._gaussian_buffers[key] = buf
+        return buf
+
+    def _get_select_buffers(self, B, H, Hkv, num_pages, device):
+        key = (B, H, Hkv, num_pages, device)
+        sb = self._select_buffers.get(key)
+        if sb is None:
+            self._select_buffers.clear()
+            sb = {
+                "page_indices": torch.zeros(B, Hkv, num_pages, dtype=torch.int32, device=device),
+                "counts": torch.zeros(B, Hkv, dtype=torch.int32, device=device),
+                "tau_floor": torch.zeros(B, H, dtype=torch.float32, device=device),
+                "cache_seqlens": torch.zeros(B, Hkv, dtype=torch.int32, device=device),
+                "tau_clamped": torch.zeros(B, H, dtype=torch.float32, device=device),
+                "effective": torch.zeros(2, dtype=torch.float32, device=device),
+            }
+            self._select_buffers[key] = sb
+        return sb
+
+    # ---------------------------------------------------------- Gaussian selection
+    def select_gaussian_aware(self, q: torch.Tensor, alpha: float = 1.5,
+                              safety_margin_z: float = 0.0, max_quantile: float = 0.99,
+                              gaussian_stats: dict = None, clamp: bool = False,
+                              last_page_size: Optional[int] = None):
+        """Gaussian threshold selection + pack (kv_cache.py:205-255).
+
+        As in the reference, ``safety_margin_z``/``max_quantile`` arguments are
+        superseded by the values in ``gaussian_stats`` (None there = automatic,
+        derived on the device from the mean sigma_global).  Returns
+        (page_indices [B, Hkv, P], num_selected [B, Hkv]); slots beyond the count
+        are unspecified.  Also fills gaussian_stats["tau_floor"], and, with
+        ``clamp``, gaussian_stats["tau_clamped"] and
+        gaussian_stats["cache_seqlens"].
+        """
+        st = gaussian_stats
+        B, H = q.shape[:2]
+        Hkv = self._k.shape[1]
+        num_pages = st["num_pages"]
+        pfs = st["pages_for_stats"]
+        sb = self._get_select_buffers(B, H, Hkv, num_pages, q.device)
+        frac = st.get("threshold_excess_margin_fraction", 0.1)
+        if last_page_size is None:
+            last_page_size = self.page_size
+        K.select_gaussian_threshold_pack(
+            st["mu_scores_per_page"], st["sigma_scores_per_page"], st["tau_hat"],
+            st["sigma_global"], self.page_size, alpha, st["safety_margin_z"], st["max_quantile"],
+            float(frac), pfs, num_pages, num_kv_heads=Hkv, out=sb["page_indices"],
+            counts=sb["counts"], tau_floor=sb["tau_floor"], cache_seqlens=sb["cache_seqlens"],
+            last_page_size=last_page_size, tau_clamped=sb["tau_clamped"] if clamp else None,
+            clamp_quantile=st.get("tau_clamp_page_max_quantile", 0.5), effective=sb["effective"])
+        st["tau_floor"] = sb["tau_floor"]
+        st["cache_seqlens"] = sb["cache_seqlens"]
+        if clamp:
+            st["tau_clamped"] = sb["tau_clamped"]
+        st["effective_margins"] = sb["effective"]
+        self.last_effective_safety_margin = (
+            sb["effective"][0] if st["safety_margin_z"] is None else st["safety_margin_z"])
+        self.last_effective_max_quantile = (
+            sb["effective"][1] if st["max_quantile"] is None else st["max_quantile"])
+        self.last_num_selected_per_head = sb["counts"]
+        return sb["page_indices"], sb["counts"]

@@ -1,0 +1,158 @@
+/* EntmaxKV for AMD Instinct MI355X (gfx950): C ABI of the sparse-entmax paged
+ * decode path.
+ *
+ * Every entry point takes raw device pointers, element strides and a
+ * hipStream_t passed as void*.  Nothing here allocates device memory:
+ * workspaces are caller-owned, sized by the *_workspace_bytes queries, and
+ * must be zero-filled once when first allocated (arrival counters inside them
+ * return to zero after every call).  Calls that share a workspace must not run
+ * concurrently.  Return value: 0 on success, EKV_ERR_ARG (-1) for a rejected
+ * argument (nothing launched), EKV_ERR_HIP (-2) for a launch failure; the
+ * message is in ekv_last_error() (thread-local).
+ *
+ * dtype codes: 0 = fp32, 1 = fp16, 2 = bf16 (storage type of q/K/V/stats).
+ * Head dim D: D / (16 / sizeof(dtype)) must be a power of two in [4, 64]
+ * (fp16/bf16: 32..512, fp32: 16..256).  GQA group H / Hkv in {1, 2, 4, 8}.
+ * Reference paths below are relative to the deep-spin/entmaxkv repository.
+ */
+#ifndef ENTMAXKV_H
+#define ENTMAXKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EKV_ABI_VERSION 1
+
+const char* ekv_last_error(void);
+int ekv_abi_version(void);
+
+/* Per-page key statistics over pages [page_begin, page_end): min, max, mean and
+ * population std (clamped >= 1e-6) of rows [p*ps, min((p+1)*ps, seq_len)).
+ * Replaces the page loop of PagedKVCache.initialize, kv_cache.py:40-70. */
+int ekv_page_stats(const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_row,
+                   void* kmin, void* kmax, void* kmean, void* kstd, int64_t s_stride_b,
+                   int64_t s_stride_h, int64_t s_stride_page, int B, int Hkv, int D, int seq_len,
+                   int page_size, int page_begin, int page_end, int dtype, void* stream);
+
+/* In-place append of one token per (b, kv head) at row `pos` (or
+ * pos_per_batch[b] when non-null, negative = skip) and recompute of that
+ * page's statistics.  K and V share strides.  Replaces the torch.cat append
+ * and last-page recompute of PagedKVCache.append, kv_cache.py:72-116. */
+int ekv_append(const void* k_new, const void* v_new, int64_t new_stride_b, int64_t new_stride_h,
+               void* k, void* v, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_row,
+               void* kmin, void* kmax, void* kmean, void* kstd, int64_t s_stride_b,
+               int64_t s_stride_h, int64_t s_stride_page, int B, int Hkv, int D, int pos,
+               const int32_t* pos_per_batch, int page_size, int dtype, void* stream);
+
+/* Page criticality scores [B, H, num_pages] (query dtype, contiguous):
+ * sum_d max(q_d kmin_pd, q_d kmax_pd) (+ ALiBi bonus when alibi_slopes [H] is
+ * non-null).  Replaces triton_estimate_page_criticality,
+ * kernels/page_criticality.py:107-187.  When k_select >= 0 the top-k page
+ * table is fused (see ekv_topk_pages) and `counters` ([B*Hkv] int32, zeroed
+ * once) is required. */
+int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kmin,
+                         const void* kmax, int64_t s_stride_b, int64_t s_stride_h,
+                         int64_t s_stride_page, const float* alibi_slopes, void* scores, int B,
+                         int H, int Hkv, int D, int num_pages, int page_size, int seq_len,
+                         int q_pos, int k_select, int last_page, int32_t* page_indices,
+                         int64_t pi_stride_b, int64_t pi_stride_h, int32_t* counters, int dtype,
+                         void* stream);
+
+/* Top-k page table per (b, kv head): the k pages with the largest score (group
+ * maximum under GQA), ascending, ties to the lower index, then `last_page`
+ * at slot k when last_page >= 0.  Replaces torch.topk + the index buffer of
+ * attention_topk.py:52-71 and kv_cache.py:167-185. */
+int ekv_topk_pages(const void* scores, int B, int H, int Hkv, int num_pages, int k, int last_page,
+                   int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h, int dtype,
+                   void* stream);
+
+/* Workspace for ekv_paged_entmax_decode. */
+int64_t ekv_decode_workspace_bytes(int B, int H, int Hkv, int D, int splits, int max_tokens);
+
+/* Paged alpha-entmax decode over the compacted page table (keyed by kv head).
+ * tau_mode 0: exact (histogram init + `iters` bracketed Halley steps), the
+ *   final tau is written to tau [B, H];
+ * tau_mode 1: tau [B, H] holds the starting value; `iters` unbounded
+ *   Halley/Newton corrections, final tau written back.
+ * qscale = (alpha-1)/sqrt(D) rounded to the storage dtype.  kv_rows bounds
+ * the rows addressable per (b, kv head); out-of-range page ids are skipped.
+ * Replaces kernels/adadecode_paged.py:567-762 and
+ * kernels/adadecode_paged_gaussian_tau.py:192-331. */
+int ekv_paged_entmax_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
+                            const void* v, int64_t kv_stride_b, int64_t kv_stride_h,
+                            int64_t kv_stride_row, int64_t kv_rows, const int32_t* page_indices,
+                            int64_t pi_stride_b, int64_t pi_stride_h, int n_slots,
+                            const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
+                            const int32_t* q_seqlens, const float* alibi_slopes, float* tau,
+                            int tau_mode, int iters, void* out, int64_t out_stride_b,
+                            int64_t out_stride_h, float alpha, float qscale, int page_size, int B,
+                            int H, int Hkv, int D, int splits, int max_tokens, void* workspace,
+                            int64_t workspace_bytes, int dtype, void* stream);
+
+/* Workspace for ekv_gaussian_page_stats. */
+int64_t ekv_gaussian_workspace_bytes(int B, int H, int Hkv, int D, int pages, int dtype);
+
+/* Per-page score moments mu_p, sigma_p [B, H, pages_for_stats] (fp32; mu_p
+ * includes the ALiBi page-mean bias when alibi_slopes is non-null), per-head
+ * mu_g, sigma_g, mean_var, var_means [B, H], and, when tau_hat is non-null,
+ * the single-Gaussian tau-hat with n = n_tokens.  Replaces
+ * compute_page_gaussian_stats_triton (kernels/gaussian_page_stats.py:128-233)
+ * and gaussian_utils.py:130-181. */
+int ekv_gaussian_page_stats(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                            const void* kmean, const void* kstd, int64_t s_stride_b,
+                            int64_t s_stride_h, int64_t s_stride_page, int pages_for_stats,
+                            const float* alibi_slopes, int page_size, int seq_len, float* mu_p,
+                            float* sigma_p, float* mu_g, float* sigma_g, float* mean_var,
+                            float* var_means, float* tau_hat, float alpha, int n_tokens,
+                            int tau_iters, float tol, int B, int H, int Hkv, int D,
+                            void* workspace, int64_t workspace_bytes, int dtype, void* stream);
+
+/* tau-hat for `count` independent single-Gaussian problems.  Replaces
+ * solve_for_tau_hat_single_gaussian_gpu, kernels/tau_solver_gpu.py:128-158. */
+int ekv_tau_single_gaussian(const float* mu_g, const float* sigma_g, float* tau_out, int count,
+                            int n_tokens, float alpha, int iterations, float tol, void* stream);
+
+/* Page-mixture tau-hat per row of [rows, pages] (uniform page count).
+ * Replaces solve_for_tau_hat_page_gaussian_mixture_triton,
+ * kernels/tau_mixture_solver_triton.py:172-240. */
+int ekv_tau_page_mixture(const float* mu_p, const float* sigma_p, float* tau_out, int rows,
+                         int pages, float page_count, float alpha, int max_iter, float tol,
+                         void* stream);
+
+/* Threshold selection + ascending pack + last-page sentinel per (b, kv head),
+ * tau floor per head, and (optional, fused) compacted cache lengths and tau
+ * clamp.  auto_margins != 0 derives safety_margin_z and the page quantile from
+ * the mean sigma_g on device (z_page_low/high are the page quantile z-values
+ * for max_quantile 0.99/0.995).  Replaces select_gaussian_threshold_pack_triton
+ * (kernels/selection_pack.py:201-272), gaussian_utils.py:163-169,
+ * clamp_tau_to_selected_page_statistics_triton (kernels/tau_clamp.py:76-151)
+ * and cache_seqlens_from_page_counts_triton (kernels/selection_pack.py:23-43). */
+int ekv_select_gaussian_pack(const float* mu_p, const float* sigma_p, const float* tau_hat,
+                             const float* sigma_g, int B, int H, int Hkv, int pages_for_stats,
+                             int num_pages, float alpha, int auto_margins, float safety_margin_z,
+                             float z_page, float z_page_low, float z_page_high,
+                             float threshold_excess_margin_fraction, int32_t* page_indices,
+                             int64_t pi_stride_b, int64_t pi_stride_h, int32_t* counts,
+                             float* tau_floor, int32_t* cache_seqlens, int page_size,
+                             int last_page_size, float* tau_clamped, float z_clamp, float eps,
+                             float* effective_margins, void* stream);
+
+/* Standalone tau clamp over a page list (kernels/tau_clamp.py:8-73). */
+int ekv_tau_clamp(const float* tau, const float* mu_p, const float* sigma_p,
+                  const int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h,
+                  int n_slots, const int32_t* num_selected, int64_t ns_stride_b,
+                  int64_t ns_stride_h, const float* tau_floor, float* out, int B, int H, int Hsel,
+                  int pages_for_stats, float alpha, float z_clamp, float eps, void* stream);
+
+/* max(count - 1, 0) * page_size + last_page_size (kernels/selection_pack.py:7-20). */
+int ekv_cache_seqlens_from_counts(const int32_t* counts, int32_t* cache_seqlens, int n,
+                                  int page_size, int last_page_size, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ENTMAXKV_H */

@@ -12,8 +12,8 @@ itself is Triton + PyTorch and cannot run here (no CUDA GPU); nothing from it
 is imported.
 
 Rounding points that the oracle reproduces on purpose:
-  * the decode query is scaled by (alpha-1)/sqrt(D) in fp32 and rounded to
-    the input dtype (kernels/adadecode_paged.py:97-98);
+  * the decode query is scaled by (alpha-1)/sqrt(D) in the input dtype
+    (constant and product rounded to it, kernels/adadecode_paged.py:97-98);
   * page statistics and criticality scores are rounded to the key / query
     dtype (kv_cache.py:48-70, kernels/page_criticality.py:168);
   * threshold selection and tau clamping compare in fp32
@@ -202,15 +202,26 @@ def topk_gqa_group_scores(scores: np.ndarray, num_kv_heads: int) -> np.ndarray:
 BINS = 16
 
 
-def decode_query_scale(alpha: float, head_dim: int) -> np.float32:
-    """fp32 constant (alpha-1)/sqrt(D) (kernels/adadecode_paged.py:79,605)."""
-    return np.float32((alpha - 1.0) * (1.0 / math.sqrt(head_dim)))
+def decode_query_scale(alpha: float, head_dim: int, dtype: str) -> float:
+    """(alpha-1)/sqrt(D) as the kernel's scalar operand (kernels/adadecode_paged.py:79,605).
+
+    The constant is a Python float multiplied with a tensor of the input
+    dtype; under Triton's scalar typing a Python scalar does not promote the
+    tensor, so the product is taken in the input dtype: the constant itself is
+    rounded to that dtype.
+    """
+    return float(round_to((alpha - 1.0) * (1.0 / math.sqrt(head_dim)), dtype))
 
 
 def scaled_query(q: np.ndarray, alpha: float, dtype: str) -> np.ndarray:
-    """q * (alpha-1)/sqrt(D) in fp32, rounded to the input dtype (adadecode_paged.py:97-98)."""
+    """q * (alpha-1)/sqrt(D) in the input dtype (kernels/adadecode_paged.py:97-98).
+
+    For fp16/bf16 the product of two representable values is exact in fp32 and
+    rounded once to the dtype; for fp32 it is the fp32 product.
+    """
     D = q.shape[-1]
-    prod = f32(q) * decode_query_scale(alpha, D)
+    c = decode_query_scale(alpha, D, dtype)
+    prod = f32(q) * np.float32(c)
     return round_to(prod.astype(np.float64), dtype)
 
 

@@ -1,0 +1,431 @@
+"""HIP path vs the CPU oracle on seeded inputs (needs an MI355X).
+
+Every test prints the case it runs before touching the GPU so a failing run
+names its case.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import entmaxkv_oracle as O
+from tests.gpu_helpers import (ATOL, TORCH_DT, assert_out_close, randn, to_dev, to_np,
+                               ulp_diff_16)
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = ["fp16", "bf16", "fp32"]
+
+
+def _case(**kw):
+    print("CASE", " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def _K():
+    from entmaxkv_amd import kernels as K
+    return K
+
+
+# ---------------------------------------------------------------------------
+# a1 / a2 page statistics
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("S", [1, 17, 1000])
+def test_page_stats_initialize(dtype, S):
+    from entmaxkv_amd import PagedKVCache
+    _case(test="page_stats", dtype=dtype, S=S)
+    rng = np.random.default_rng(S)
+    B, H, D = 2, 3, 128
+    k = randn(rng, (B, H, S, D), dtype)
+    v = randn(rng, (B, H, S, D), dtype)
+    cache = PagedKVCache(page_size=16)
+    cache.initialize(to_dev(k, dtype), to_dev(v, dtype))
+    torch.cuda.synchronize()
+    ref = O.page_stats(k, 16, dtype)
+    got = [cache.k_min, cache.k_max, cache.k_mean, cache.k_std]
+    for name, g, r in zip(["min", "max", "mean", "std"], got, ref):
+        g = to_np(g)
+        assert g.shape == r.shape
+        if name in ("min", "max"):
+            np.testing.assert_array_equal(g, r)
+        else:
+            assert ulp_diff_16(g, r, dtype).max() <= 1.0, name
+    np.testing.assert_array_equal(to_np(cache.k_cache), k)
+    np.testing.assert_array_equal(to_np(cache.v_cache), v)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_append_in_place_matches_rebuild(dtype):
+    from entmaxkv_amd import PagedKVCache
+    _case(test="append", dtype=dtype)
+    rng = np.random.default_rng(3)
+    B, H, D, S0, steps = 2, 4, 64, 30, 40
+    k = randn(rng, (B, H, S0 + steps, D), dtype)
+    v = randn(rng, (B, H, S0 + steps, D), dtype)
+    cache = PagedKVCache(page_size=16, capacity=S0 + 8)  # forces a capacity growth
+    kd, vd = to_dev(k, dtype), to_dev(v, dtype)
+    cache.initialize(kd[:, :, :S0], vd[:, :, :S0])
+    for t in range(S0, S0 + steps):
+        cache.append(kd[:, :, t:t + 1], vd[:, :, t:t + 1])
+    torch.cuda.synchronize()
+    assert cache.k_cache.shape[2] == S0 + steps
+    np.testing.assert_array_equal(to_np(cache.k_cache), k)
+    np.testing.assert_array_equal(to_np(cache.v_cache), v)
+    ref = O.page_stats(k, 16, dtype)
+    for g, r in zip([cache.k_min, cache.k_max, cache.k_mean, cache.k_std], ref):
+        assert ulp_diff_16(to_np(g), r, dtype).max() <= 1.0
+
+
+# ---------------------------------------------------------------------------
+# a3 / a4 criticality + top-k
+# ---------------------------------------------------------------------------
+
+def _build_cache(rng, B, Hkv, S, D, dtype, k_scale=1.0):
+    from entmaxkv_amd import PagedKVCache
+    k = randn(rng, (B, Hkv, S, D), dtype, k_scale)
+    v = randn(rng, (B, Hkv, S, D), dtype)
+    cache = PagedKVCache(page_size=16)
+    cache.initialize(to_dev(k, dtype), to_dev(v, dtype))
+    return cache, k, v
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("G", [1, 4])
+@pytest.mark.parametrize("alibi", [False, True])
+def test_criticality_and_topk(dtype, G, alibi):
+    _case(test="criticality_topk", dtype=dtype, G=G, alibi=alibi)
+    rng = np.random.default_rng(10 + G)
+    B, Hkv, S, D = 2, 2, 16 * 300 + 5, 128
+    H = Hkv * G
+    cache, k, v = _build_cache(rng, B, Hkv, S, D, dtype)
+    q = randn(rng, (B, H, 1, D), dtype)
+    qd = to_dev(q, dtype)
+    slopes = None
+    if alibi:
+        slopes = np.exp2(-8.0 * np.arange(1, H + 1) / H).astype(np.float32)
+    kk = 64
+    pidx = cache.select_topk(qd, kk, alibi_slopes=None if slopes is None else torch.tensor(slopes, device="cuda"))
+    torch.cuda.synchronize()
+    P = cache.num_pages
+    kmin, kmax = O.page_stats(k, 16, dtype)[:2]
+    ref_scores = O.page_criticality(q[:, :, 0], kmin, kmax, dtype, num_pages=P - 1,
+                                    alibi_slopes=slopes, page_size=16, seq_len=S, q_pos=S - 1)
+    got_scores = to_np(cache.last_page_scores)
+    assert ulp_diff_16(got_scores, ref_scores, dtype).max() <= 1.0
+    # the page table is bit-exact given the scores the kernel produced
+    group = O.topk_gqa_group_scores(got_scores, Hkv)
+    ref_sel = O.topk_pages(group, kk)
+    got = to_np(pidx).astype(np.int64)
+    np.testing.assert_array_equal(got[:, :, :kk], ref_sel)
+    assert (got[:, :, kk] == P - 1).all()
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_topk_ties_and_edges(dtype):
+    K = _K()
+    _case(test="topk_ties", dtype=dtype)
+    rng = np.random.default_rng(4)
+    B, H, P = 2, 2, 1000
+    s = O.round_to(np.round(rng.standard_normal((B, H, P)) * 4) / 4, dtype)  # many ties
+    s[0, 0, 10] = np.nan
+    sd = to_dev(s, dtype)
+    for k in (0, 1, 37, 500, 999, 1000):
+        out = K.topk_pages(sd, k, H, last_page=P)
+        torch.cuda.synchronize()
+        got = to_np(out).astype(np.int64)
+        ref = O.topk_pages(s, k)
+        np.testing.assert_array_equal(got[:, :, :k], ref, err_msg=f"k={k}")
+        assert (got[:, :, k] == P).all()
+
+
+# ---------------------------------------------------------------------------
+# a6 / a13 paged decode
+# ---------------------------------------------------------------------------
+
+def _decode_case(rng, dtype, B, Hkv, G, S, D, n_sel, k_scale=1.0):
+    H = Hkv * G
+    K_ = randn(rng, (B, Hkv, S, D), dtype, k_scale)
+    V_ = randn(rng, (B, Hkv, S, D), dtype)
+    q = randn(rng, (B, H, 1, D), dtype)
+    P = (S + 15) // 16
+    pidx = np.stack([np.stack([np.concatenate([np.sort(rng.choice(P - 1, n_sel, replace=False)), [P - 1]])
+                               for _ in range(Hkv)]) for _ in range(B)])
+    lps = S - (P - 1) * 16
+    seqlens = np.full((B, Hkv), n_sel * 16 + lps)
+    return K_, V_, q, pidx, seqlens
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("alpha", [1.5, 2.0])
+@pytest.mark.parametrize("G", [1, 4])
+@pytest.mark.parametrize("niter", [2, 10])
+def test_decode_exact_matches_oracle(dtype, alpha, G, niter):
+    K = _K()
+    _case(test="decode_exact", dtype=dtype, alpha=alpha, G=G, niter=niter)
+    rng = np.random.default_rng(100 + G)
+    B, Hkv, S, D = 2, 2, 16 * 200 + 3, 128
+    Kc, Vc, q, pidx, seqlens = _decode_case(rng, dtype, B, Hkv, G, S, D, 64)
+    H = Hkv * G
+    dt = TORCH_DT[dtype]
+    out = torch.zeros(B, H, 1, D, dtype=dt, device="cuda")
+    taus = torch.zeros(B, H, dtype=torch.float32, device="cuda")
+    K.sparse_attention_decode_paged(to_dev(q, dtype), to_dev(Kc, dtype), to_dev(Vc, dtype), out,
+                                    torch.tensor(seqlens, dtype=torch.int32, device="cuda"),
+                                    torch.tensor(pidx, dtype=torch.int32, device="cuda"), 16,
+                                    alpha=alpha, niter=niter, taus_out=taus)
+    torch.cuda.synchronize()
+    ref, ref_tau = O.paged_entmax_decode(q[:, :, 0], Kc, Vc, pidx, seqlens, 16, alpha, niter, dtype)
+    assert_out_close(to_np(out)[:, :, 0], ref, dtype)
+    np.testing.assert_allclose(to_np(taus), ref_tau, atol=1e-4)
+    if niter == 10:
+        # converged: equals exact sort-based entmax over the selected tokens
+        qs = O.scaled_query(q[:, :, 0], alpha, dtype)
+        for b in range(B):
+            for h in range(H):
+                rows = O.compacted_rows(pidx[b, h // G], seqlens[b, h // G], 16)
+                s = Kc[b, h // G][rows] @ qs[b, h]
+                p = O.entmax_exact(s, alpha)
+                assert_out_close(to_np(out)[b, h, 0], p @ Vc[b, h // G][rows], dtype, "exact")
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+@pytest.mark.parametrize("iters", [0, 1, 2])
+def test_decode_given_tau_matches_oracle(dtype, iters):
+    K = _K()
+    _case(test="decode_given_tau", dtype=dtype, iters=iters)
+    rng = np.random.default_rng(7)
+    B, Hkv, S, D = 2, 4, 16 * 100, 64
+    Kc, Vc, q, pidx, seqlens = _decode_case(rng, dtype, B, Hkv, 1, S, D, 40)
+    tau0 = O.paged_entmax_decode(q[:, :, 0], Kc, Vc, pidx, seqlens, 16, 1.5, 30, dtype)[1] - 0.05
+    tau = torch.tensor(tau0, dtype=torch.float32, device="cuda").contiguous()
+    out = torch.zeros(B, Hkv, 1, D, dtype=TORCH_DT[dtype], device="cuda")
+    K.sparse_attention_decode_paged_gaussian_tau(
+        to_dev(q, dtype), to_dev(Kc, dtype), to_dev(Vc, dtype), out,
+        torch.tensor(seqlens, dtype=torch.int32, device="cuda"),
+        torch.tensor(pidx, dtype=torch.int32, device="cuda"), 16, tau, alpha=1.5,
+        tau_correction_iters=iters)
+    torch.cuda.synchronize()
+    ref, ref_tau = O.paged_entmax_decode(q[:, :, 0], Kc, Vc, pidx, seqlens, 16, 1.5, 0, dtype,
+                                         tau_given=tau0, tau_iters=iters)
+    assert_out_close(to_np(out)[:, :, 0], ref, dtype)
+    np.testing.assert_allclose(to_np(tau), ref_tau, atol=1e-5)
+
+
+def test_decode_edge_cases():
+    """Empty and single-token heads, partial last page, out-of-range page ids."""
+    K = _K()
+    _case(test="decode_edges")
+    rng = np.random.default_rng(9)
+    dtype = "fp16"
+    B, Hkv, S, D = 1, 4, 16 * 10 + 1, 128
+    Kc = randn(rng, (B, Hkv, S, D), dtype)
+    Vc = randn(rng, (B, Hkv, S, D), dtype)
+    q = randn(rng, (B, Hkv, 1, D), dtype)
+    pidx = np.array([[[3, 10, 0], [10, 0, 0], [2, 10, 0], [999999, 10, 0]]])
+    seqlens = np.array([[17, 1, 0, 17]])
+    out = torch.full((B, Hkv, 1, D), 7.0, dtype=torch.float16, device="cuda")
+    K.sparse_attention_decode_paged(to_dev(q, dtype), to_dev(Kc, dtype), to_dev(Vc, dtype), out,
+                                    torch.tensor(seqlens, dtype=torch.int32, device="cuda"),
+                                    torch.tensor(pidx, dtype=torch.int32, device="cuda"), 16,
+                                    alpha=1.5, niter=10)
+    torch.cuda.synchronize()
+    o = to_np(out)[0, :, 0]
+    # head 1: a single token gets probability 1 -> out = v
+    np.testing.assert_allclose(o[1], Vc[0, 1, 160], atol=2e-3)
+    # head 2: no tokens -> zeros
+    assert np.all(o[2] == 0)
+    # head 0: page 3 + first row of page 10
+    ref, _ = O.paged_entmax_decode(q[:, :1, 0], Kc[:, :1], Vc[:, :1], pidx[:, :1], seqlens[:, :1],
+                                   16, 1.5, 10, dtype)
+    assert_out_close(o[0], ref[0, 0], dtype)
+    # head 3: the malformed page id is skipped, the last page still attends
+    ref3, _ = O.paged_entmax_decode(q[:, 3:4, 0], Kc[:, 3:4], Vc[:, 3:4], np.array([[[10]]]),
+                                    np.array([[1]]), 16, 1.5, 10, dtype)
+    assert_out_close(o[3], ref3[0, 0], dtype)
+
+
+# ---------------------------------------------------------------------------
+# public top-k API end to end
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype,G", [("fp16", 1), ("bf16", 4), ("fp32", 1)])
+def test_topk_api_end_to_end(dtype, G):
+    from entmaxkv_amd import sparse_attention_decode_paged
+    _case(test="topk_api", dtype=dtype, G=G)
+    rng = np.random.default_rng(21)
+    B, Hkv, S0, D, ps = 2, 2, 16 * 128, 128, 16
+    H = Hkv * G
+    cache, k, v = _build_cache(rng, B, Hkv, S0, D, dtype)
+    q = randn(rng, (B, H, 1, D), dtype)
+    kn = randn(rng, (B, Hkv, 1, D), dtype)
+    vn = randn(rng, (B, Hkv, 1, D), dtype)
+    budget = 512
+    S = S0 + 1
+    P = (S + ps - 1) // ps
+    n_sel = min(budget // ps, P - 1)
+    lps = S - (P - 1) * ps
+    out = torch.zeros(B, H, 1, D, dtype=TORCH_DT[dtype], device="cuda")
+    sparse_attention_decode_paged(
+        to_dev(q, dtype), cache, to_dev(kn, dtype), to_dev(vn, dtype), out, budget,
+        torch.full((B,), n_sel * ps + lps, dtype=torch.int32, device="cuda"),
+        torch.full((B,), S, dtype=torch.int32, device="cuda"), alpha=1.5, niter=10,
+        append_cache=True)
+    torch.cuda.synchronize()
+    Kf = np.concatenate([k, kn], axis=2)
+    Vf = np.concatenate([v, vn], axis=2)
+    st = O.page_stats(Kf, ps, dtype)
+    scores = to_np(cache.last_page_scores)
+    ref_scores = O.page_criticality(q[:, :, 0], st[0], st[1], dtype, num_pages=P - 1)
+    assert ulp_diff_16(scores, ref_scores, dtype).max() <= 1.0
+    sel = O.topk_pages(O.topk_gqa_group_scores(scores, Hkv), n_sel)
+    pidx = np.concatenate([sel, np.full((B, Hkv, 1), P - 1)], axis=2)
+    np.testing.assert_array_equal(to_np(cache._page_indices_buf).astype(np.int64), pidx)
+    ref, _ = O.paged_entmax_decode(q[:, :, 0], Kf, Vf, pidx, np.full((B, Hkv), n_sel * ps + lps),
+                                   ps, 1.5, 10, dtype, q_seqlens=np.full(B, S))
+    assert_out_close(to_np(out)[:, :, 0], ref, dtype)
+
+
+# ---------------------------------------------------------------------------
+# a7 - a12 Gaussian path
+# ---------------------------------------------------------------------------
+
+def _gaussian_inputs(rng, dtype, B, H, S, D, outlier_frac=0.0):
+    k = rng.standard_normal((B, H, S, D)) + rng.standard_normal((B, H, 1, 1)) * math.sqrt(0.5)
+    q = rng.standard_normal((B, H, 1, D))
+    if outlier_frac:
+        P = S // 16
+        for b in range(B):
+            for h in range(H):
+                pages = rng.choice(P, max(1, int(outlier_frac * P)), replace=False)
+                for p in pages:
+                    qh = q[b, h, 0] / np.linalg.norm(q[b, h, 0])
+                    k[b, h, p * 16:(p + 1) * 16] = 3.0 * (k[b, h, p * 16:(p + 1) * 16] + 4.0 * qh)
+    return O.round_to(q, dtype), O.round_to(k, dtype), randn(rng, (B, H, S, D), dtype)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+@pytest.mark.parametrize("alpha", [1.5, 2.0])
+def test_gaussian_stats_tau_select_clamp(dtype, alpha):
+    K = _K()
+    from entmaxkv_amd import PagedKVCache
+    from entmaxkv_amd.gaussian_utils import compute_gaussian_aware_statistics
+    _case(test="gaussian_pipeline", dtype=dtype, alpha=alpha)
+    rng = np.random.default_rng(31)
+    B, H, S, D, ps = 2, 4, 16 * 256 + 1, 128, 16
+    q, k, v = _gaussian_inputs(rng, dtype, B, H, S, D, outlier_frac=0.02)
+    cache = PagedKVCache(page_size=ps)
+    cache.initialize(to_dev(k, dtype), to_dev(v, dtype))
+    qd = to_dev(q, dtype)
+    st = compute_gaussian_aware_statistics(qd, cache.k_mean, cache.k_std, S, ps, alpha=alpha,
+                                           buffers=cache.get_gaussian_buffers(qd, cache.num_pages - 1))
+    lps = O.last_page_size(S, ps)
+    pidx, counts = cache.select_gaussian_aware(qd, alpha=alpha, gaussian_stats=st, clamp=True,
+                                               last_page_size=lps)
+    torch.cuda.synchronize()
+    P = cache.num_pages
+    pfs = P - 1
+    kst = O.page_stats(k, ps, dtype)
+    ref = O.gaussian_page_stats(q[:, :, 0], kst[2], kst[3], pfs)
+    mu_p, sg_p = to_np(st["mu_scores_per_page"]), to_np(st["sigma_scores_per_page"])
+    np.testing.assert_allclose(mu_p, ref["mu_p"], rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(sg_p, ref["sigma_p"], rtol=1e-5, atol=1e-6)
+    sg_g = to_np(st["sigma_global"])[..., 0]
+    mu_g = to_np(st["mu_global"])[..., 0]
+    np.testing.assert_allclose(mu_g, ref["mu_g"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(sg_g, ref["sigma_g"], rtol=1e-5)
+    # tau-hat from the GPU's own global moments
+    th = to_np(st["tau_hat"])
+    ref_th = O.tau_single_gaussian(mu_g, sg_g, pfs * ps, alpha)
+    np.testing.assert_allclose(th, ref_th, atol=2e-5, rtol=2e-5)
+    # auto margins, tau floor
+    smz, mq = O.auto_selection_margins(sg_g)
+    eff = to_np(st["effective_margins"])
+    np.testing.assert_allclose(eff, [smz, mq], rtol=1e-5)
+    tf = to_np(st["tau_floor"])
+    ref_tf = O.tau_floor_fp32(mu_p, sg_p, th, sg_g, alpha, np.float32(eff[0]), 0.2, pfs)
+    np.testing.assert_allclose(tf, ref_tf, atol=1e-5, rtol=1e-5)
+    # selection: bit-exact given the GPU's moments and floor
+    z_page = O.page_quantile_z(0.995 if eff[1] > 0.992 else 0.99, ps)
+    packed, ref_counts = O.select_gaussian_pages(mu_p, sg_p, tf, alpha, z_page, pfs, P)
+    got_pidx = to_np(pidx).astype(np.int64)
+    got_counts = to_np(counts).astype(np.int64)
+    np.testing.assert_array_equal(got_counts, ref_counts)
+    for b in range(B):
+        for h in range(H):
+            np.testing.assert_array_equal(got_pidx[b, h, :got_counts[b, h]], packed[b, h])
+    np.testing.assert_array_equal(to_np(st["cache_seqlens"]),
+                                  O.cache_seqlens_from_counts(ref_counts, ps, lps))
+    ref_tc = O.tau_clamp(th, mu_p, sg_p, packed, ref_counts, tf, alpha,
+                         O.page_quantile_z(0.5, ps), pfs)
+    np.testing.assert_allclose(to_np(st["tau_clamped"]), ref_tc, atol=1e-6, rtol=1e-6)
+    # standalone clamp entry point agrees with the fused one
+    tc2 = K.clamp_tau_to_selected_page_statistics(st["tau_hat"], st["mu_scores_per_page"],
+                                                   st["sigma_scores_per_page"], pidx, counts,
+                                                   st["tau_floor"], ps, alpha, 0.5, pfs)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_np(tc2), to_np(st["tau_clamped"]))
+
+
+@pytest.mark.parametrize("tau_mode", ["exact", "fixed", "corrected"])
+def test_gaussian_api_end_to_end(tau_mode):
+    from entmaxkv_amd import PagedKVCache, sparse_attention_decode_gaussian_aware_entmax
+    _case(test="gaussian_api", tau_mode=tau_mode)
+    dtype = "fp16"
+    rng = np.random.default_rng(41)
+    B, H, S, D, ps = 2, 4, 16 * 128 + 1, 128, 16
+    q, k, v = _gaussian_inputs(rng, dtype, B, H, S, D, outlier_frac=0.02)
+    cache = PagedKVCache(page_size=ps)
+    cache.initialize(to_dev(k, dtype), to_dev(v, dtype))
+    out = torch.zeros(B, H, 1, D, dtype=torch.float16, device="cuda")
+    sparse_attention_decode_gaussian_aware_entmax(to_dev(q, dtype), cache, None, None, out,
+                                                  alpha=1.5, tau_mode=tau_mode)
+    torch.cuda.synchronize()
+    st = cache.last_gaussian_stats
+    counts = to_np(st["cache_seqlens"]).astype(np.int64)
+    nslots = to_np(cache.last_num_selected_per_head).astype(np.int64)
+    pidx = to_np(cache._select_buffers[next(iter(cache._select_buffers))]["page_indices"]).astype(np.int64)
+    for b in range(B):
+        for h in range(H):
+            pidx[b, h, nslots[b, h]:] = 0
+    if tau_mode == "exact":
+        ref, _ = O.paged_entmax_decode(q[:, :, 0], k, v, pidx, counts, ps, 1.5, 2, dtype)
+    else:
+        tau0 = to_np(st["tau_clamped"])
+        iters = 0 if tau_mode == "fixed" else 1
+        ref, _ = O.paged_entmax_decode(q[:, :, 0], k, v, pidx, counts, ps, 1.5, 0, dtype,
+                                       tau_given=tau0, tau_iters=iters)
+    assert_out_close(to_np(out)[:, :, 0], ref, dtype)
+
+
+def test_tau_mixture_matches_oracle():
+    K = _K()
+    _case(test="tau_mixture")
+    rng = np.random.default_rng(51)
+    mu = rng.standard_normal((3, 200)).astype(np.float32)
+    sg = (np.abs(rng.standard_normal((3, 200))) + 0.1).astype(np.float32)
+    for alpha in (1.5, 2.0):
+        got = K.solve_for_tau_hat_page_gaussian_mixture(torch.tensor(mu, device="cuda"),
+                                                        torch.tensor(sg, device="cuda"),
+                                                        alpha=alpha, uniform_page_count=16.0)
+        torch.cuda.synchronize()
+        ref = O.tau_page_mixture(mu, sg, 16.0, alpha)
+        np.testing.assert_allclose(to_np(got)[:, 0], ref, atol=5e-5, rtol=5e-5)
+
+
+def test_tau_single_matches_oracle():
+    K = _K()
+    _case(test="tau_single")
+    mu = np.array([0.1, -0.5, 0.0, 2.0, 0.3], np.float32)
+    sg = np.array([0.3, 1.2, 0.05, 0.7, 2.5], np.float32)
+    for alpha in (1.5, 2.0):
+        for n in (16, 2048, 32768):
+            got = K.solve_for_tau_hat_single_gaussian_gpu(torch.tensor(mu, device="cuda"),
+                                                          torch.tensor(sg, device="cuda"), n, alpha)
+            torch.cuda.synchronize()
+            ref = O.tau_single_gaussian(mu, sg, n, alpha)
+            np.testing.assert_allclose(to_np(got), ref, atol=2e-5, rtol=2e-5)
