@@ -14,7 +14,9 @@ import threading
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libentmaxkv_hip.so")
+# ENTMAXKV_AMD_LIB selects another build of the same library (e.g. a variant
+# built for an experiment); the default is the in-tree build.
+LIB_PATH = os.environ.get("ENTMAXKV_AMD_LIB", os.path.join(_HERE, "libentmaxkv_hip.so"))
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -29,11 +31,11 @@ SIGNATURES = {
     "ekv_append": (I, [P, P, I64, I64, P, P, I64, I64, I64, P, P, P, P, I64, I64, I64,
                        I, I, I, I, P, I, I, P]),
     "ekv_page_criticality": (I, [P, I64, I64, P, P, I64, I64, I64, P, P, I, I, I, I, I, I, I, I,
-                                 I, I, P, I64, I64, P, I, P]),
+                                 I, I, P, I64, I64, I, P]),
     "ekv_topk_pages": (I, [P, I, I, I, I, I, I, P, I64, I64, I, P]),
     "ekv_decode_workspace_bytes": (I64, [I, I, I, I, I, I]),
     "ekv_paged_entmax_decode": (I, [P, I64, I64, P, P, I64, I64, I64, I64, P, I64, I64, I,
-                                    P, I64, I64, P, P, P, I, I, P, I64, I64, F, F, I, I, I, I,
+                                    P, I64, I64, P, P, P, P, I, I, P, I64, I64, F, F, I, I, I, I,
                                     I, I, I, P, I64, I, P]),
     "ekv_gaussian_workspace_bytes": (I64, [I, I, I, I, I, I]),
     "ekv_gaussian_page_stats": (I, [P, I64, I64, P, P, I64, I64, I64, I, P, I, I, P, P, P, P, P,

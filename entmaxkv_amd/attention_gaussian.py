@@ -94,11 +94,12 @@ def sparse_attention_decode_gaussian_aware_entmax(
                 tau_correction_iters = 0
             else:
                 tau_correction_iters = 1 if alibi_slopes is None else 2
-        tau = gaussian_stats["tau_clamped"] if do_clamp else gaussian_stats["tau_hat"].clone()
+        tau0 = gaussian_stats["tau_clamped"] if do_clamp else gaussian_stats["tau_hat"]
         K.paged_entmax_decode(
             q, kv_cache._k, kv_cache._v, out, cache_seqlens, page_indices, page_size, alpha,
-            tau_mode=1, iters=tau_correction_iters, tau=tau, alibi_slopes=alibi_slopes,
-            q_seqlens=q_seqlens, workspace=workspace, kv_rows=kv_cache.kv_capacity)
-        gaussian_stats["tau_final"] = tau
+            tau_mode=1, iters=tau_correction_iters, tau=workspace.taus, tau_in=tau0,
+            alibi_slopes=alibi_slopes, q_seqlens=q_seqlens, workspace=workspace,
+            kv_rows=kv_cache.kv_capacity)
+        gaussian_stats["tau_final"] = workspace.taus
     kv_cache.last_gaussian_stats = gaussian_stats
     return out

@@ -1,26 +1,28 @@
 """Builds libentmaxkv_hip.so (gfx950) from entmaxkv_amd/csrc/*.hip with hipcc.
 
 Usage: python -m entmaxkv_amd.build   (or call build()).
-The library is written next to this file so it travels with the source tree.
+Each source compiles in parallel to an object under entmaxkv_amd/_build/, then
+one link writes the library next to this file so it travels with the tree.
 """
 
 from __future__ import annotations
 
+import concurrent.futures as cf
 import glob
 import os
 import subprocess
-import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
+OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libentmaxkv_hip.so")
 ARCH = "gfx950"
 
-FLAGS = [
-    "-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
+CFLAGS = [
+    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     # packed fp32 arithmetic is disabled for every kernel in this library
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-ffp-contract=fast", "-Wno-unused-result",
+    "-Wno-unused-result",
 ]
 
 
@@ -30,16 +32,33 @@ def hipcc() -> str:
     return cand if os.path.exists(cand) else "hipcc"
 
 
-def build(verbose: bool = False) -> str:
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *FLAGS, "-I", os.path.join(HERE, "..", "include"), *srcs, "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
+def _run(cmd):
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed ({res.returncode})")
+        raise RuntimeError(f"hipcc failed ({res.returncode}): {' '.join(cmd)}\n"
+                           f"{res.stdout}{res.stderr}")
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(OBJ, exist_ok=True)
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    inc = ["-I", os.path.join(HERE, "..", "include")]
+    objs, cmds = [], []
+    for src in srcs:
+        obj = os.path.join(OBJ, os.path.basename(src) + ".o")
+        objs.append(obj)
+        cmds.append([hipcc(), *CFLAGS, *inc, "-c", src, "-o", obj])
+    workers = min(len(cmds), max(1, (os.cpu_count() or 2)))
+    with cf.ThreadPoolExecutor(workers) as ex:
+        for cmd, fut in zip(cmds, [ex.submit(_run, c) for c in cmds]):
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            fut.result()
+    tmp = LIB + ".tmp"
+    link = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]
+    if verbose:
+        print(" ".join(link), flush=True)
+    _run(link)
     os.replace(tmp, LIB)
     return LIB
 

@@ -88,6 +88,72 @@ template <typename T> struct VecRaw {
 };
 
 // ---------------------------------------------------------------------------
+// 16-byte dot products in the storage format (exact 16-bit products,
+// fp32 accumulation: v_dot2_f32_f16 / v_dot2_f32_bf16; fp32 uses fma)
+// ---------------------------------------------------------------------------
+
+typedef _Float16 ekv_half2 __attribute__((ext_vector_type(2)));
+typedef short ekv_short2 __attribute__((ext_vector_type(2)));
+
+template <typename T> struct Dot16;
+template <> struct Dot16<_Float16> {
+  static __device__ __forceinline__ float dot(const uint4& a, const uint4& b, float acc) {
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(ekv_half2, a.x), __builtin_bit_cast(ekv_half2, b.x), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(ekv_half2, a.y), __builtin_bit_cast(ekv_half2, b.y), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(ekv_half2, a.z), __builtin_bit_cast(ekv_half2, b.z), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(ekv_half2, a.w), __builtin_bit_cast(ekv_half2, b.w), acc, false);
+    return acc;
+  }
+  // per-element all-ones mask where the element is >= 0 (+0.0 and -0.0 included)
+  static __device__ __forceinline__ uint4 nonneg_mask(const uint4& q) {
+    auto m = [](uint32_t w) {
+      const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+      const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+      return ((float)lo >= 0.f ? 0x0000ffffu : 0u) | ((float)hi >= 0.f ? 0xffff0000u : 0u);
+    };
+    return make_uint4(m(q.x), m(q.y), m(q.z), m(q.w));
+  }
+};
+template <> struct Dot16<bf16_t> {
+  static __device__ __forceinline__ float dot(const uint4& a, const uint4& b, float acc) {
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ekv_short2, a.x), __builtin_bit_cast(ekv_short2, b.x), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ekv_short2, a.y), __builtin_bit_cast(ekv_short2, b.y), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ekv_short2, a.z), __builtin_bit_cast(ekv_short2, b.z), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ekv_short2, a.w), __builtin_bit_cast(ekv_short2, b.w), acc, false);
+    return acc;
+  }
+  static __device__ __forceinline__ uint4 nonneg_mask(const uint4& q) {
+    auto m = [](uint32_t w) {
+      const float lo = __uint_as_float(w << 16);
+      const float hi = __uint_as_float(w & 0xffff0000u);
+      return (lo >= 0.f ? 0x0000ffffu : 0u) | (hi >= 0.f ? 0xffff0000u : 0u);
+    };
+    return make_uint4(m(q.x), m(q.y), m(q.z), m(q.w));
+  }
+};
+template <> struct Dot16<float> {
+  static __device__ __forceinline__ float dot(const uint4& a, const uint4& b, float acc) {
+    acc = fmaf(__uint_as_float(a.x), __uint_as_float(b.x), acc);
+    acc = fmaf(__uint_as_float(a.y), __uint_as_float(b.y), acc);
+    acc = fmaf(__uint_as_float(a.z), __uint_as_float(b.z), acc);
+    acc = fmaf(__uint_as_float(a.w), __uint_as_float(b.w), acc);
+    return acc;
+  }
+  static __device__ __forceinline__ uint4 nonneg_mask(const uint4& q) {
+    auto m = [](uint32_t w) { return __uint_as_float(w) >= 0.f ? 0xffffffffu : 0u; };
+    return make_uint4(m(q.x), m(q.y), m(q.z), m(q.w));
+  }
+};
+
+// Element-wise (mask ? b : a) on 16-byte vectors (v_bfi_b32).
+__device__ __forceinline__ uint4 bit_select(const uint4& a, const uint4& b, const uint4& mask) {
+  return make_uint4((b.x & mask.x) | (a.x & ~mask.x), (b.y & mask.y) | (a.y & ~mask.y),
+                    (b.z & mask.z) | (a.z & ~mask.z), (b.w & mask.w) | (a.w & ~mask.w));
+}
+
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// ---------------------------------------------------------------------------
 // wave-level reductions (wave64)
 // ---------------------------------------------------------------------------
 
@@ -168,32 +234,48 @@ __device__ __forceinline__ float block_sum(float x, float* scratch) {
 // cross-workgroup completion
 // ---------------------------------------------------------------------------
 
-// Called by every thread of a workgroup after it has written its results.
-// Returns true in exactly one workgroup per counter: the last of `total`
-// arrivals.  That workgroup resets the counter to zero and, after return, sees
-// the global writes of all other arrivals (agent-scope release/acquire).
+// Cross-workgroup data inside one kernel goes through agent-coherent stores
+// and loads (relaxed atomics at agent scope: the stores write through to the
+// device coherence point, the loads bypass non-coherent cache levels).  This
+// avoids agent-scope fences, which on gfx950 write back and invalidate whole
+// L2 caches.
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ld_coherent(const int* p) {
+  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent_u16(uint16_t* p, uint16_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint16_t ld_coherent_u16(const uint16_t* p) {
+  return __hip_atomic_load(const_cast<uint16_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Called by every thread of a workgroup after it has issued its coherent
+// stores.  Each wave waits for its stores to complete, then one thread bumps
+// the arrival counter.  Returns true in exactly one workgroup per counter: the
+// last of `total` arrivals, which resets the counter to zero and may then read
+// every other arrival's coherent stores with ld_coherent.
 __device__ __forceinline__ bool last_arrival(int* counter, int total) {
   __shared__ int s_last;
-  __threadfence();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    int last = (prev == total - 1);
+    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = (prev == total - 1);
     if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = last;
   }
   __syncthreads();
-  const bool last = s_last != 0;
-  if (last) __threadfence();
-  return last;
-}
-
-// Loads that must observe other workgroups' writes made in the same kernel.
-__device__ __forceinline__ float ld_acquire(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int ld_acquire(const int* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return s_last != 0;
 }
 
 // ---------------------------------------------------------------------------

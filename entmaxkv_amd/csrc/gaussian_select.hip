@@ -31,8 +31,10 @@ constexpr int kUnroll = 4;
 __device__ __forceinline__ float normal_pdf(float x) {
   return expf(-0.5f * x * x) * 0.3989422804014327f;
 }
+// Phi(x) = 0.5 * erfc(-x / sqrt(2)): equal to 0.5 * (1 + erf(x / sqrt(2))) but
+// without the cancellation of 1 + erf in the lower tail.
 __device__ __forceinline__ float normal_cdf(float x) {
-  return 0.5f * (1.0f + erff(x * 0.7071067811865476f));
+  return 0.5f * erfcf(-x * 0.7071067811865476f);
 }
 
 // f(tau) = n*E[[(alpha-1)S - tau]_+^(1/(alpha-1))] - 1 for S ~ N(mu, sigma^2)
@@ -212,7 +214,7 @@ __global__ __launch_bounds__(kThreads) void gaussian_stats_kernel(StatsArgs a) {
     for (int r = lane; r < SEGS * kUnroll; r += 64) x += red[qn][g][r];
     x = wave_sum(x);
     if (lane == 0)
-      a.ws_tiles[(((int64_t)b * a.H + h0 + g) * gridDim.x + blockIdx.x) * 3 + qn] = x;
+      st_coherent(a.ws_tiles + (((int64_t)b * a.H + h0 + g) * gridDim.x + blockIdx.x) * 3 + qn, x);
   }
   if (!last_arrival(&a.counters[bkv], gridDim.x)) return;
 
@@ -221,9 +223,9 @@ __global__ __launch_bounds__(kThreads) void gaussian_stats_kernel(StatsArgs a) {
     const float* tl = a.ws_tiles + ((int64_t)b * a.H + h) * gridDim.x * 3;
     float s0 = 0.f, s1 = 0.f, s2 = 0.f;
     for (int t = lane; t < (int)gridDim.x; t += 64) {
-      s0 += tl[t * 3 + 0];
-      s1 += tl[t * 3 + 1];
-      s2 += tl[t * 3 + 2];
+      s0 += ld_coherent(tl + t * 3 + 0);
+      s1 += ld_coherent(tl + t * 3 + 1);
+      s2 += ld_coherent(tl + t * 3 + 2);
     }
     s0 = wave_sum(s0);
     s1 = wave_sum(s1);

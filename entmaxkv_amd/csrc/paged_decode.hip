@@ -1,4 +1,4 @@
-// Paged split-KV alpha-entmax decode over a compacted page table.
+// Paged alpha-entmax decode over a compacted page table.
 //
 // Follows kernels/adadecode_paged.py:567-762 (exact tau: global max,
 // 16-bin histogram init, bracketed Halley, output) and
@@ -6,32 +6,50 @@
 // Halley/Newton corrections, output).  Compacted token c of (b, kv head) lives
 // in cache row page_indices[c / ps] * ps + c % ps; scores are
 // s_c = qs . k_c with qs = q * (alpha-1)/sqrt(D) rounded to the input dtype,
-// the output is out = sum_c [s_c - tau]_+^(1/(alpha-1)) v_c (not renormalised,
-// as in the reference).
+// and out = sum_c [s_c - tau]_+^(1/(alpha-1)) v_c (not renormalised, as in
+// the reference).
 //
-// Two kernels instead of the reference's 7 + 2*niter launches:
-//   score_tau_kernel  grid (splits, B*Hkv): each workgroup streams its share
-//     of the selected K rows once (16-byte loads, all G query heads of the
-//     group served by one load) and writes fp32 scores to the workspace; the
-//     last workgroup of a (b, kv head) solves tau for the group's heads over
-//     the L2-resident scores, one wave per head.
-//   weighted_sum_kernel  grid (splits, B*Hkv): each workgroup re-reads its
-//     scores, compacts the tokens with s > tau (the entmax support), gathers
-//     only those V rows, and writes a per-split fp32 partial; the last
-//     workgroup sums the partials in split order (deterministic, no atomics)
-//     and writes out in the input dtype.
-// K is read once and V only on the support; the reference reads K 3+niter
-// times.
+// One workgroup of 512 threads owns one (b, kv head) and all G query heads
+// of its group, so nothing crosses workgroups:
+//   phase 1  stream the selected K rows once (16-byte loads, one load serves
+//            all G heads) and keep the fp32 scores in LDS (in the workspace
+//            when they do not fit);
+//   phase 2  solve tau per head over those scores (one wave per head, or the
+//            whole workgroup per head for long token lists);
+//   phase 3  compact the tokens with s > tau (the entmax support), gather only
+//            those V rows and reduce in registers/LDS; write out.
+// When batch * kv heads is too small to fill the GPU, phase 1 runs as a
+// separate split launch over many workgroups per head (score_split_kernel)
+// and the head kernel starts at phase 2.  The reference launches 7 + 2*niter
+// kernels and reads K 3 + niter times.
 #include "ekv_common.h"
 #include "../../include/entmaxkv.h"
 
 using namespace ekv;
 
+#ifdef EKV_PHASE_TIMERS
+// experiment builds only: per-workgroup phase timestamps (wall clock, 100 MHz)
+__device__ unsigned long long ekv_phase_timers[4096 * 8];
+#define EKV_STAMP(i) \
+  if (threadIdx.x == 0 && blockIdx.x < 4096) ekv_phase_timers[blockIdx.x * 8 + (i)] = wall_clock64()
+extern "C" int ekv_debug_phase_timers(unsigned long long* host, int n) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(ekv_phase_timers), n * sizeof(unsigned long long));
+}
+#else
+#define EKV_STAMP(i)
+#endif
+
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
+constexpr int kSplitThreads = 256;
+constexpr int kSplitUnroll = 4;
+constexpr int kHeadThreads = 512;
+constexpr int kWaves = kHeadThreads / 64;
 constexpr int kBins = 16;
+constexpr int kBatch = 8;           // independent loads per lane in score passes
+constexpr int kWaveTauMax = 4096;   // longer token lists solve tau with the whole workgroup
+constexpr int kHeadPathMinHeads = 128;
+constexpr int kTablePages = 2048;   // page ids staged in LDS per phase-1 chunk
 
 struct DecodeArgs {
   const void* q;
@@ -47,8 +65,9 @@ struct DecodeArgs {
   int64_t csb, csh;
   const int32_t* q_seqlens;
   const float* slopes;
-  float* tau;  // [B, H]
-  int tau_mode;  // 0 exact (histogram + bracketed Halley), 1 given tau (unbounded Halley)
+  float* tau;           // [B, H] output
+  const float* tau_in;  // [B, H] starting tau (given-tau mode)
+  int tau_mode;         // 0 exact (histogram + bracketed Halley), 1 given tau (unbounded Halley)
   int iters;
   void* out;
   int64_t osb, osh;
@@ -56,12 +75,11 @@ struct DecodeArgs {
   float qscale;  // (alpha-1)/sqrt(D) already rounded to the input dtype
   int page_size;
   int H, Hkv;
-  int splits;
-  int max_tokens;
-  float* ws_scores;   // [B, H, max_tokens]
-  float* ws_partial;  // [B, H, splits, D]
-  int* ws_flags;      // [B, Hkv, splits]
-  int* counters;      // [2, B, Hkv]
+  int splits;        // phase-1 workgroups per head in the split path
+  int max_tokens;    // row stride of the workspace scores
+  float* ws_scores;  // [B, H, max_tokens]
+  int stage_cap;     // scores per head kept in LDS (0: workspace)
+  int scores_ready;  // phase 1 already done by score_split_kernel
 };
 
 __device__ __forceinline__ int token_count(const DecodeArgs& a, int b, int kvh) {
@@ -79,47 +97,99 @@ __device__ __forceinline__ int64_t token_row(const int32_t* __restrict__ pi, int
   return (page >= 0 && row < row_limit) ? row : -1;
 }
 
-// entmax weight of an active score difference x > 0
 __device__ __forceinline__ float entmax_weight(float x, float alpha, float c0) {
   if (alpha == 2.0f) return x;
   if (alpha == 1.5f) return x * x;
   return exp2f(log2f(x) * c0);
 }
 
-// ---------------------------------------------------------------------------
-// tau solve for one head, executed by one full wave over L2-resident scores
-// ---------------------------------------------------------------------------
-
-__device__ __forceinline__ void accumulate(const float* __restrict__ sc, int n, float t, float alpha,
-                                           float c0, float& a0, float& a1, float& a2) {
-  const int lane = threadIdx.x & 63;
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f;
-  for (int c = lane; c < n; c += 64) {
-    const float x = sc[c];
-    if (x > t) {
-      const float d = x - t;
-      if (alpha == 2.0f) {
-        s0 += d;
-        s1 += 1.f;
-      } else if (alpha == 1.5f) {
-        s0 += d * d;
-        s1 += d;
-        s2 += 1.f;
-      } else {
-        const float l = log2f(d);
-        s0 += exp2f(l * c0);
-        s1 += exp2f(l * (c0 - 1.f));
-        s2 += exp2f(l * (c0 - 2.f));
-      }
-    }
+// q * qscale rounded to the storage dtype, kept in the storage format
+// (kernels/adadecode_paged.py:97-98).
+template <typename T, int G>
+__device__ __forceinline__ void load_query(const DecodeArgs& a, int b, int h0, int col,
+                                           uint4 (&qraw)[G]) {
+  constexpr int VEC = 16 / sizeof(T);
+  const T* qb = (const T*)a.q + b * a.qsb;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    Vec<T> x;
+    x.load(qb + (h0 + g) * a.qsh + col);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) x.v[i] = x.v[i] * a.qscale;
+    T tmp[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) tmp[i] = from_f<T>(x.v[i]);
+    qraw[g] = *reinterpret_cast<const uint4*>(tmp);
   }
-  a0 = wave_sum(s0);
-  a1 = wave_sum(s1);
-  a2 = wave_sum(s2);
 }
 
-// kernels/adadecode.py:38-112 (alpha 2, 1.5 and generic bin search)
-__device__ void histogram_init(const int* hist, float gmax, float alpha, float& t, float& t_lo,
+// Scores of compacted tokens [c_begin, c_end) of one (b, kv head) for its G
+// heads: sc[g * stride + c].  NT threads, rows of LPR lanes, U rows per
+// segment in flight.  `pages` holds the page ids of tokens from `c_base` on
+// (LDS or global memory).
+template <typename T, int LPR, int G, int NT, int U, typename PagePtr>
+__device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, int c_begin,
+                                           int c_end, float* sc, int64_t stride, PagePtr pages,
+                                           int c_base) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int SEGS = NT / LPR;
+  constexpr int ROWS = SEGS * U;
+  const int seg = threadIdx.x / LPR;
+  const int sl = threadIdx.x % LPR;
+  const int col = sl * VEC;
+  const int h0 = kvh * G;
+  uint4 qraw[G];
+  load_query<T, G>(a, b, h0, col, qraw);
+  float slope[G];
+  int q_idx = 0;
+  if (a.slopes) {
+    q_idx = (a.q_seqlens ? a.q_seqlens[b] : a.cache_seqlens[b * a.csb + kvh * a.csh]) - 1;
+#pragma unroll
+    for (int g = 0; g < G; ++g) slope[g] = a.slopes[h0 + g] * (a.alpha - 1.0f);
+  }
+  const T* kh = (const T*)a.k + b * a.ksb + kvh * a.ksh;
+  const int ps = a.page_size;
+  for (int c0 = c_begin; c0 < c_end; c0 += ROWS) {
+    uint4 kv[U];
+    int rows[U];  // row within the (b, kv head); the cache holds < 2^31 rows per head
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * SEGS + seg;
+      rows[u] = -1;
+      if (c < c_end) {
+        const int page = pages[(c - c_base) / ps];
+        const int64_t row = (int64_t)page * ps + (c % ps);
+        rows[u] = (page >= 0 && row < a.row_limit) ? (int)row : -1;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (rows[u] >= 0) kv[u] = ld16(kh + (int64_t)rows[u] * a.ksr + col);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * SEGS + seg;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float acc = rows[u] >= 0 ? Dot16<T>::dot(qraw[g], kv[u], 0.f) : 0.f;
+        acc = seg_sum<LPR>(acc);
+        if (c < c_end && sl == 0) {
+          float s = acc;
+          if (rows[u] < 0) s = -INFINITY;
+          else if (a.slopes) s += slope[g] * (float)(rows[u] - q_idx);
+          sc[g * stride + c] = s;
+        }
+      }
+    }
+    if (c0 == c_begin) EKV_STAMP(2);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// tau: kernels/adadecode.py:12-112, 381-426, 555-592 and
+// kernels/adadecode_paged_gaussian_tau.py:12-53
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ void histogram_init(const int* hist, float gmax, float alpha, float& t, float& t_lo,
                                float& t_hi) {
   const float t0 = gmax - 1.0f;
   if (alpha == 2.0f || alpha == 1.5f) {
@@ -189,7 +259,6 @@ __device__ void histogram_init(const int* hist, float gmax, float alpha, float& 
   t = 0.5f * (t_lo + t_hi);
 }
 
-// kernels/adadecode.py:12-35
 __device__ __forceinline__ void halley_bisect(float& t, float& t_lo, float& t_hi, float a0,
                                               float a1, float a2, float c0, float c1) {
   const float ff = a0 - 1.0f;
@@ -202,7 +271,6 @@ __device__ __forceinline__ void halley_bisect(float& t, float& t_lo, float& t_hi
   t = good ? new_t : 0.5f * (t_lo + t_hi);
 }
 
-// kernels/adadecode_paged_gaussian_tau.py:12-53
 __device__ __forceinline__ float halley_unbounded(float t, float a0, float a1, float a2, float c0,
                                                   float c1) {
   const float ff = a0 - 1.0f;
@@ -217,248 +285,342 @@ __device__ __forceinline__ float halley_unbounded(float t, float a0, float a1, f
   return tn;
 }
 
-__device__ void solve_tau_wave(const DecodeArgs& a, const float* __restrict__ sc, int n,
-                               float tau_in, int* hist, float& tau_out) {
-  const int lane = threadIdx.x & 63;
+// Reduction scope of a tau solve: one wave (lanes stride 64) or the whole
+// workgroup (threads stride NT, block reductions through LDS).
+struct WaveScope {
+  static __device__ __forceinline__ int first() { return threadIdx.x & 63; }
+  static constexpr int kStride = 64;
+  static __device__ __forceinline__ float sum(float x, float*) { return wave_sum(x); }
+  static __device__ __forceinline__ float max(float x, float*) { return wave_max(x); }
+  static __device__ __forceinline__ void sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
+};
+
+template <int NT>
+struct BlockScope {
+  static __device__ __forceinline__ int first() { return threadIdx.x; }
+  static constexpr int kStride = NT;
+  static __device__ __forceinline__ float sum(float x, float* scratch) {
+    return block_sum(x, scratch);
+  }
+  static __device__ __forceinline__ float max(float x, float* scratch) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    x = wave_max(x);
+    if (lane == 0) scratch[wid] = x;
+    __syncthreads();
+    float r = -INFINITY;
+    for (int w = 0; w < NT / 64; ++w) r = fmaxf(r, scratch[w]);
+    __syncthreads();
+    return r;
+  }
+  static __device__ __forceinline__ void sync() { __syncthreads(); }
+};
+
+// One pass over scores[0..n) of a head: the sums of [s - t]_+^(1/(alpha-1) - j)
+// for j = 0, 1, 2 (kernels/adadecode_paged.py:357-372), branch-free per score.
+template <typename S>
+__device__ __forceinline__ void accumulate_pass(const float* __restrict__ sc, int n, float t,
+                                                float alpha, float c0, float* scratch, float& a0,
+                                                float& a1, float& a2) {
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+  const bool generic = !(alpha == 2.0f || alpha == 1.5f);
+  const bool sparsemax = alpha == 2.0f;
+  for (int b0 = 0; b0 < n; b0 += S::kStride * kBatch) {
+    float x[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int c = b0 + j * S::kStride + S::first();
+      x[j] = c < n ? sc[c] : -INFINITY;
+    }
+    if (!generic) {
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const bool act = x[j] > t;
+        const float d = act ? x[j] - t : 0.f;
+        const float one = act ? 1.f : 0.f;
+        s0 += sparsemax ? d : d * d;
+        s1 += sparsemax ? one : d;
+        s2 += sparsemax ? 0.f : one;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        if (x[j] > t) {
+          const float l = log2f(x[j] - t);
+          s0 += exp2f(l * c0);
+          s1 += exp2f(l * (c0 - 1.f));
+          s2 += exp2f(l * (c0 - 2.f));
+        }
+      }
+    }
+  }
+  a0 = S::sum(s0, scratch);
+  a1 = S::sum(s1, scratch);
+  a2 = S::sum(s2, scratch);
+}
+
+template <typename S>
+__device__ __forceinline__ float solve_tau(const DecodeArgs& a, const float* __restrict__ sc,
+                                           int n, float tau_in, int* hist, float* scratch) {
   const float alpha = a.alpha;
   const float c0 = 1.0f / (alpha - 1.0f);
   const float c1 = c0 - 1.0f;
   float t;
   if (a.tau_mode == 0) {
     float m = -1.0e6f;
-    for (int c = lane; c < n; c += 64) m = fmaxf(m, sc[c]);
-    const float gmax = wave_max(m);
-    const float t0 = gmax - 1.0f;
-    if (lane < kBins) hist[lane] = 0;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    for (int c = lane; c < n; c += 64) {
-      const float f = (sc[c] - t0) * (float)kBins;
-      if (f > -1.0f) atomicAdd(&hist[min((int)f, kBins - 1)], 1);
+    for (int b0 = 0; b0 < n; b0 += S::kStride * kBatch) {
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int c = b0 + j * S::kStride + S::first();
+        if (c < n) m = fmaxf(m, sc[c]);
+      }
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-    __builtin_amdgcn_wave_barrier();
+    const float gmax = S::max(m, scratch);
+    EKV_STAMP(4);
+    const float t0 = gmax - 1.0f;
+    if (S::first() < kBins) hist[S::first()] = 0;
+    S::sync();
+    for (int b0 = 0; b0 < n; b0 += S::kStride * kBatch) {
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int c = b0 + j * S::kStride + S::first();
+        if (c < n) {
+          const float f = (sc[c] - t0) * (float)kBins;
+          if (f > -1.0f) atomicAdd(&hist[min((int)f, kBins - 1)], 1);
+        }
+      }
+    }
+    S::sync();
     float t_lo, t_hi;
+    EKV_STAMP(5);
     histogram_init(hist, gmax, alpha, t, t_lo, t_hi);
     for (int it = 0; it < a.iters; ++it) {
       float a0, a1, a2;
-      accumulate(sc, n, t, alpha, c0, a0, a1, a2);
+      accumulate_pass<S>(sc, n, t, alpha, c0, scratch, a0, a1, a2);
       halley_bisect(t, t_lo, t_hi, a0, a1, a2, c0, c1);
     }
   } else {
     t = tau_in;
     for (int it = 0; it < a.iters; ++it) {
       float a0, a1, a2;
-      accumulate(sc, n, t, alpha, c0, a0, a1, a2);
+      accumulate_pass<S>(sc, n, t, alpha, c0, scratch, a0, a1, a2);
       t = halley_unbounded(t, a0, a1, a2, c0, c1);
     }
   }
-  tau_out = t;
+  return t;
 }
 
 // ---------------------------------------------------------------------------
-// kernel 1: scores + tau
+// phase 1 as its own launch (few heads)
 // ---------------------------------------------------------------------------
 
 template <typename T, int LPR, int G>
-__global__ __launch_bounds__(kThreads) void score_tau_kernel(DecodeArgs a) {
-  constexpr int VEC = 16 / sizeof(T);
-  constexpr int SEGS = kThreads / LPR;
-  constexpr int ROWS = SEGS * kUnroll;
-  __shared__ int hist[kThreads / 64][kBins];
-  const int seg = threadIdx.x / LPR;
-  const int sl = threadIdx.x % LPR;
-  const int col = sl * VEC;
+__global__ __launch_bounds__(kSplitThreads) void score_split_kernel(DecodeArgs a) {
   const int split = blockIdx.x;
   const int bkv = blockIdx.y;
   const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
-  const int h0 = kvh * G;
   const int n = token_count(a, b, kvh);
   const int per = (n + a.splits - 1) / a.splits;
   const int c_start = split * per;
   const int c_end = min(c_start + per, n);
-
-  if (c_start < c_end) {
-    const T* qb = (const T*)a.q + b * a.qsb;
-    float qv[G][VEC];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      Vec<T> x;
-      x.load(qb + (h0 + g) * a.qsh + col);
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) qv[g][i] = to_f<T>(from_f<T>(x.v[i] * a.qscale));
-    }
-    float slope[G];
-    int q_idx = 0;
-    if (a.slopes) {
-      q_idx = (a.q_seqlens ? a.q_seqlens[b] : a.cache_seqlens[b * a.csb + kvh * a.csh]) - 1;
-#pragma unroll
-      for (int g = 0; g < G; ++g) slope[g] = a.slopes[h0 + g] * (a.alpha - 1.0f);
-    }
-    const int32_t* pi = a.page_indices + b * a.pisb + kvh * a.pish;
-    const T* kh = (const T*)a.k + b * a.ksb + kvh * a.ksh;
-    float* sc0 = a.ws_scores + ((int64_t)b * a.H + h0) * a.max_tokens;
-
-    for (int c0 = c_start; c0 < c_end; c0 += ROWS) {
-      VecRaw<T> kv[kUnroll];
-      int64_t rows[kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int c = c0 + u * SEGS + seg;
-        rows[u] = (c < c_end) ? token_row(pi, c, a.page_size, a.row_limit) : -1;
-        if (rows[u] >= 0) kv[u].load(kh + rows[u] * a.ksr + col);
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int c = c0 + u * SEGS + seg;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float acc = 0.f;
-          if (rows[u] >= 0) {
-#pragma unroll
-            for (int i = 0; i < VEC; ++i) acc += qv[g][i] * kv[u].get(i);
-          }
-          acc = seg_sum<LPR>(acc);
-          if (c < c_end && sl == 0) {
-            float s = acc;
-            if (rows[u] < 0) s = -INFINITY;
-            else if (a.slopes) s += slope[g] * (float)(rows[u] - q_idx);
-            sc0[(int64_t)g * a.max_tokens + c] = s;
-          }
-        }
-      }
-    }
-  }
-
-  if (!last_arrival(&a.counters[bkv], a.splits)) return;
-
-  // tau for the group's heads: one wave per head
-  const int wid = threadIdx.x >> 6;
-  for (int g0 = 0; g0 < G; g0 += kThreads / 64) {
-    const int g = g0 + wid;
-    if (g < G) {
-      const int h = h0 + g;
-      const float* sc = a.ws_scores + ((int64_t)b * a.H + h) * a.max_tokens;
-      float* tp = a.tau + b * a.H + h;
-      const float tin = (a.tau_mode == 1) ? *tp : 0.f;
-      float tout;
-      solve_tau_wave(a, sc, n, tin, hist[wid], tout);
-      if ((threadIdx.x & 63) == 0) *tp = tout;
-    }
-  }
+  if (c_start >= c_end) return;
+  float* sc = a.ws_scores + ((int64_t)b * a.H + kvh * G) * a.max_tokens;
+  const int32_t* pi = a.page_indices + b * a.pisb + kvh * a.pish;
+  score_rows<T, LPR, G, kSplitThreads, kSplitUnroll>(a, b, kvh, c_start, c_end, sc, a.max_tokens,
+                                                     pi, 0);
 }
 
 // ---------------------------------------------------------------------------
-// kernel 2: support gather of V + deterministic split reduction
+// the head kernel
 // ---------------------------------------------------------------------------
 
-template <typename T, int LPR, int G>
-__global__ __launch_bounds__(kThreads) void weighted_sum_kernel(DecodeArgs a) {
+struct HeadShared {
+  int (*hist)[kBins];
+  float* scratch;
+  float* s_tau;
+  int64_t* sup_row;
+  float* sup_p;  // [G][kHeadThreads]
+  int* flag_cnt;
+  float* red;    // [kWaves][D]
+  int* s_pages;  // [kTablePages]
+};
+
+// Phases 1-3 of one (b, kv head); `sc` points to LDS when kStaged (so every
+// score access is a ds_* instruction) and to the workspace otherwise.
+template <typename T, int LPR, int G, int U, bool kStaged>
+__device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int kvh, int n,
+                                                 float* sc, int64_t stride, const HeadShared& sh) {
   constexpr int VEC = 16 / sizeof(T);
-  constexpr int SEGS = kThreads / LPR;
+  constexpr int SEGS = kHeadThreads / LPR;
   constexpr int D = LPR * VEC;
-  __shared__ int64_t sup_row[kThreads];
-  __shared__ float sup_p[G][kThreads];
-  __shared__ float red[SEGS][D];
-  __shared__ int scan_scratch[kThreads / 64 + 1];
-
   const int tid = threadIdx.x;
-  const int seg = tid / LPR;
-  const int col = (tid % LPR) * VEC;
-  const int split = blockIdx.x;
-  const int bkv = blockIdx.y;
-  const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
+  const int lane = tid & 63, wid = tid >> 6;
   const int h0 = kvh * G;
-  const int n = token_count(a, b, kvh);
-  const int per = (n + a.splits - 1) / a.splits;
-  const int c_start = split * per;
-  const int c_end = min(c_start + per, n);
-  const float alpha = a.alpha;
-  const float c0 = 1.0f / (alpha - 1.0f);
+  const int ps = a.page_size;
+  const int32_t* pi = a.page_indices + b * a.pisb + kvh * a.pish;
 
+  EKV_STAMP(0);
+  // phase 1: scores, the page table staged in LDS chunk by chunk
+  if (!a.scores_ready) {
+    for (int cb = 0; cb < n; cb += kTablePages * ps) {
+      const int ce = min(n, cb + kTablePages * ps);
+      const int np = (ce - cb + ps - 1) / ps;
+      for (int i = tid; i < np; i += kHeadThreads) sh.s_pages[i] = pi[cb / ps + i];
+      __syncthreads();
+      EKV_STAMP(1);
+      score_rows<T, LPR, G, kHeadThreads, U>(a, b, kvh, cb, ce, sc, stride, sh.s_pages, cb);
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+  EKV_STAMP(3);
+
+  // phase 2: tau per head
+  if (n <= kWaveTauMax) {
+    for (int g = wid; g < G; g += kWaves) {
+      const float tin = a.tau_mode == 1 ? a.tau_in[b * a.H + h0 + g] : 0.f;
+      const float t = solve_tau<WaveScope>(a, sc + g * stride, n, tin, sh.hist[wid], nullptr);
+      if (lane == 0) sh.s_tau[g] = t;
+    }
+  } else {
+    for (int g = 0; g < G; ++g) {
+      const float tin = a.tau_mode == 1 ? a.tau_in[b * a.H + h0 + g] : 0.f;
+      const float t = solve_tau<BlockScope<kHeadThreads>>(a, sc + g * stride, n, tin, sh.hist[0],
+                                                          sh.scratch);
+      if (tid == 0) sh.s_tau[g] = t;
+      __syncthreads();
+    }
+  }
+  __syncthreads();
   float tau[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) tau[g] = a.tau[b * a.H + h0 + g];
+  for (int g = 0; g < G; ++g) tau[g] = sh.s_tau[g];
+  if (tid < G) a.tau[b * a.H + h0 + tid] = sh.s_tau[tid];
+  EKV_STAMP(6);
 
+  // phase 3: gather the support's V rows
+  const float alpha = a.alpha;
+  const float c0 = 1.0f / (alpha - 1.0f);
+  const int seg = tid / LPR;
+  const int col = (tid % LPR) * VEC;
+  const T* vh = (const T*)a.v + b * a.ksb + kvh * a.ksh;
   float acc[G][VEC];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int i = 0; i < VEC; ++i) acc[g][i] = 0.f;
 
-  const int32_t* pi = a.page_indices + b * a.pisb + kvh * a.pish;
-  const T* vh = (const T*)a.v + b * a.ksb + kvh * a.ksh;
-  const float* sc0 = a.ws_scores + ((int64_t)b * a.H + h0) * a.max_tokens;
-  int support = 0;
-
-  for (int t0 = c_start; t0 < c_end; t0 += kThreads) {
+  for (int t0 = 0; t0 < n; t0 += kHeadThreads) {
     const int c = t0 + tid;
     float p[G];
     bool any = false;
     int64_t row = -1;
-    if (c < c_end) {
-      row = token_row(pi, c, a.page_size, a.row_limit);
+    if (c < n) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float s = sc0[(int64_t)g * a.max_tokens + c];
+        const float s = sc[g * stride + c];
         p[g] = 0.f;
         if (s > tau[g]) {
           p[g] = entmax_weight(s - tau[g], alpha, c0);
           any = true;
         }
       }
-      if (row < 0) any = false;
+      if (any) {
+        row = token_row(pi, c, ps, a.row_limit);
+        if (row < 0) any = false;
+      }
     }
-    int nsup;
-    const int slot = block_excl_scan(any ? 1 : 0, scan_scratch, &nsup);
-    if (any) {
-      sup_row[slot] = row;
+    const uint64_t m = __ballot(any);
+    if (lane == 0) sh.flag_cnt[wid] = __popcll(m);
+    __syncthreads();
+    int before = 0, nsup = 0;
 #pragma unroll
-      for (int g = 0; g < G; ++g) sup_p[g][slot] = p[g];
+    for (int w = 0; w < kWaves; ++w) {
+      const int cw = sh.flag_cnt[w];
+      before += (w < wid) ? cw : 0;
+      nsup += cw;
+    }
+    if (any) {
+      const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+      const int slot = before + __popcll(m & below);
+      sh.sup_row[slot] = row;
+#pragma unroll
+      for (int g = 0; g < G; ++g) sh.sup_p[g * kHeadThreads + slot] = p[g];
     }
     __syncthreads();
-    for (int j = seg; j < nsup; j += SEGS) {
-      Vec<T> x;
-      x.load(vh + sup_row[j] * a.ksr + col);
+    for (int j0 = seg; j0 < nsup; j0 += 2 * SEGS) {
+      const int j1 = j0 + SEGS;
+      Vec<T> x0, x1;
+      x0.load(vh + sh.sup_row[j0] * a.ksr + col);
+      if (j1 < nsup) x1.load(vh + sh.sup_row[j1] * a.ksr + col);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float w = sup_p[g][j];
+        const float w0 = sh.sup_p[g * kHeadThreads + j0];
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[g][i] += w * x.v[i];
+        for (int i = 0; i < VEC; ++i) acc[g][i] += w0 * x0.v[i];
+        if (j1 < nsup) {
+          const float w1 = sh.sup_p[g * kHeadThreads + j1];
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) acc[g][i] += w1 * x1.v[i];
+        }
       }
     }
-    support += nsup;
     __syncthreads();
   }
+  EKV_STAMP(3);
 
-  float* part = a.ws_partial + (((int64_t)b * a.H + h0) * a.splits + split) * D;
-  if (support > 0) {
+  // reduce the row segments: within each wave by shuffles, then across waves
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+  for (int g = 0; g < G; ++g) {
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) red[seg][col + i] = acc[g][i];
-      __syncthreads();
-      for (int e = tid; e < D; e += kThreads) {
-        float r = 0.f;
-        for (int s2 = 0; s2 < SEGS; ++s2) r += red[s2][e];
-        part[(int64_t)g * a.splits * D + e] = r;
-      }
-      __syncthreads();
+    for (int i = 0; i < VEC; ++i) {
+      float x = acc[g][i];
+#pragma unroll
+      for (int o = LPR; o < 64; o <<= 1) x += __shfl_xor(x, o, 64);
+      acc[g][i] = x;
     }
+    if (lane < LPR) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) sh.red[wid * D + col + i] = acc[g][i];
+    }
+    __syncthreads();
+    for (int e = tid; e < D; e += kHeadThreads) {
+      float r = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) r += sh.red[w * D + e];
+      T* o = (T*)a.out + b * a.osb + (h0 + g) * a.osh;
+      o[e] = from_f<T>(r);
+    }
+    __syncthreads();
   }
-  if (tid == 0) a.ws_flags[(int64_t)bkv * a.splits + split] = support > 0 ? 1 : 0;
+}
 
-  if (!last_arrival(&a.counters[gridDim.y + bkv], a.splits)) return;
+template <typename T, int LPR, int G, int U>
+__global__ __launch_bounds__(kHeadThreads) void decode_head_kernel(DecodeArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int D = LPR * VEC;
+  extern __shared__ float stage[];  // [G][stage_cap] scores when staged
+  __shared__ int hist[kWaves][kBins];
+  __shared__ float scratch[kWaves + 1];
+  __shared__ float s_tau[G];
+  __shared__ int64_t sup_row[kHeadThreads];
+  __shared__ float sup_p[G * kHeadThreads];
+  __shared__ int flag_cnt[kWaves];
+  __shared__ float red[kWaves * D];
+  __shared__ int s_pages[kTablePages];
+  const HeadShared sh{hist, scratch, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
 
-  const int* flags = a.ws_flags + (int64_t)bkv * a.splits;
-  for (int e = tid; e < G * D; e += kThreads) {
-    const int g = e / D, d = e % D;
-    const float* pg = a.ws_partial + (((int64_t)b * a.H + h0 + g) * a.splits) * D + d;
-    float r = 0.f;
-    for (int s2 = 0; s2 < a.splits; ++s2)
-      if (flags[s2]) r += pg[(int64_t)s2 * D];
-    T* o = (T*)a.out + b * a.osb + (h0 + g) * a.osh;
-    o[d] = from_f<T>(r);
+  const int bkv = blockIdx.x;
+  const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
+  const int n = token_count(a, b, kvh);
+  if (!a.scores_ready && n <= a.stage_cap) {
+    decode_head_body<T, LPR, G, U, true>(a, b, kvh, n, stage, a.stage_cap, sh);
+  } else {
+    float* ws = a.ws_scores + ((int64_t)b * a.H + kvh * G) * a.max_tokens;
+    decode_head_body<T, LPR, G, U, false>(a, b, kvh, n, ws, a.max_tokens, sh);
   }
 }
 
@@ -473,16 +635,18 @@ int dispatch_group(int G, F&& f) {
   }
 }
 
+// LDS per workgroup on gfx950, and the part of it given to staged scores.
+constexpr int kLdsPerWorkgroup = 160 * 1024;
+constexpr int kStageBytes = 96 * 1024;
+
 }  // namespace
 
 extern "C" int64_t ekv_decode_workspace_bytes(int B, int H, int Hkv, int D, int splits,
                                               int max_tokens) {
-  const int64_t scores = (int64_t)B * H * max_tokens * 4;
-  const int64_t partial = (int64_t)B * H * splits * D * 4;
-  const int64_t flags = (int64_t)B * Hkv * splits * 4;
-  const int64_t counters = (int64_t)2 * B * Hkv * 4;
-  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
-  return up(counters) + up(flags) + up(scores) + up(partial);
+  (void)Hkv;
+  (void)D;
+  (void)splits;
+  return ((int64_t)B * H * max_tokens * 4 + 255) / 256 * 256;
 }
 
 extern "C" int ekv_paged_entmax_decode(
@@ -490,30 +654,22 @@ extern "C" int ekv_paged_entmax_decode(
     int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
     const int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h, int n_slots,
     const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
-    const int32_t* q_seqlens, const float* alibi_slopes, float* tau, int tau_mode, int iters,
-    void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale,
-    int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens, void* workspace,
-    int64_t workspace_bytes, int dtype, void* stream) {
+    const int32_t* q_seqlens, const float* alibi_slopes, const float* tau_in, float* tau,
+    int tau_mode, int iters, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha,
+    float qscale, int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens,
+    void* workspace, int64_t workspace_bytes, int dtype, void* stream) {
   EKV_REQUIRE(q && k && v && page_indices && cache_seqlens && tau && out && workspace,
               "ekv_paged_entmax_decode: null pointer");
   EKV_REQUIRE(B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0, "ekv_paged_entmax_decode: bad heads");
   EKV_REQUIRE(page_size > 0 && n_slots > 0 && splits > 0 && max_tokens > 0,
               "ekv_paged_entmax_decode: bad sizes");
   EKV_REQUIRE(tau_mode == 0 || tau_mode == 1, "ekv_paged_entmax_decode: tau_mode %d", tau_mode);
+  EKV_REQUIRE(tau_mode == 0 || tau_in, "ekv_paged_entmax_decode: given-tau mode needs tau_in");
   EKV_REQUIRE(iters >= 0, "ekv_paged_entmax_decode: iters %d", iters);
   EKV_REQUIRE(alpha > 1.0f, "ekv_paged_entmax_decode: alpha must be > 1");
   EKV_REQUIRE(workspace_bytes >= ekv_decode_workspace_bytes(B, H, Hkv, D, splits, max_tokens),
               "ekv_paged_entmax_decode: workspace too small");
-  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
-  char* w = (char*)workspace;
   DecodeArgs a;
-  a.counters = (int*)w;
-  w += up((int64_t)2 * B * Hkv * 4);
-  a.ws_flags = (int*)w;
-  w += up((int64_t)B * Hkv * splits * 4);
-  a.ws_scores = (float*)w;
-  w += up((int64_t)B * H * max_tokens * 4);
-  a.ws_partial = (float*)w;
   a.q = q;
   a.qsb = q_stride_b;
   a.qsh = q_stride_h;
@@ -533,6 +689,7 @@ extern "C" int ekv_paged_entmax_decode(
   a.q_seqlens = q_seqlens;
   a.slopes = alibi_slopes;
   a.tau = tau;
+  a.tau_in = tau_in;
   a.tau_mode = tau_mode;
   a.iters = iters;
   a.out = out;
@@ -545,19 +702,47 @@ extern "C" int ekv_paged_entmax_decode(
   a.Hkv = Hkv;
   a.splits = splits;
   a.max_tokens = max_tokens;
+  a.ws_scores = (float*)workspace;
   hipStream_t s = (hipStream_t)stream;
+  const int G = H / Hkv;
+  const bool head_path = B * Hkv >= kHeadPathMinHeads;
+  const int cap = kStageBytes / 4 / (G > 0 ? G : 1);
+  a.stage_cap = head_path ? (max_tokens < cap ? max_tokens : cap) : 0;
+  a.scores_ready = head_path ? 0 : 1;
   return dispatch_dtype(dtype, [&](auto tv) {
     using T = decltype(tv);
     return dispatch_lpr<T>(D, [&](auto lpr) {
       constexpr int LPR = decltype(lpr)::value;
-      return dispatch_group(H / Hkv, [&](auto gv) {
-        constexpr int G = decltype(gv)::value;
-        dim3 grid(splits, B * Hkv);
-        hipLaunchKernelGGL((score_tau_kernel<T, LPR, G>), grid, dim3(kThreads), 0, s, a);
-        int rc = check_launch("score_tau_kernel");
-        if (rc) return rc;
-        hipLaunchKernelGGL((weighted_sum_kernel<T, LPR, G>), grid, dim3(kThreads), 0, s, a);
-        return check_launch("weighted_sum_kernel");
+      return dispatch_group(G, [&](auto gv) {
+        constexpr int GG = decltype(gv)::value;
+        constexpr int U = GG >= 4 ? 4 : 32 / GG;
+        if (!head_path) {
+          hipLaunchKernelGGL((score_split_kernel<T, LPR, GG>), dim3(splits, B * Hkv),
+                             dim3(kSplitThreads), 0, s, a);
+          int rc = check_launch("score_split_kernel");
+          if (rc) return rc;
+        }
+        auto kern = decode_head_kernel<T, LPR, GG, U>;
+        if (a.stage_cap > 0) {
+          // LDS left for staged scores next to the kernel's static LDS
+          hipFuncAttributes attr;
+          hipError_t e = hipFuncGetAttributes(&attr, (const void*)kern);
+          if (e != hipSuccess)
+            return set_error(EKV_ERR_HIP, "decode_head_kernel attributes: %s", hipGetErrorString(e));
+          const int64_t avail = (int64_t)kLdsPerWorkgroup - (int64_t)attr.sharedSizeBytes;
+          const int64_t fit = avail > 0 ? avail / (4 * GG) : 0;
+          if (fit < a.stage_cap) a.stage_cap = (int)fit;
+        }
+        const size_t lds = (size_t)a.stage_cap * GG * sizeof(float);
+        if (lds > 0) {
+          hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+          if (e != hipSuccess)
+            return set_error(EKV_ERR_HIP, "decode_head_kernel LDS %zu: %s", lds,
+                             hipGetErrorString(e));
+        }
+        hipLaunchKernelGGL(kern, dim3(B * Hkv), dim3(kHeadThreads), lds, s, a);
+        return check_launch("decode_head_kernel");
       });
     });
   });

@@ -87,8 +87,8 @@ def estimate_page_criticality(q, k_min, k_max, alibi_slopes=None, q_pos: int = 0
     """Upper-bound page scores [B, H, P(-1)] in the query dtype.
 
     Mirrors triton_estimate_page_criticality (kernels/page_criticality.py:107-187,
-    apply_scaling=False).  ``topk=(k, last_page, page_indices, counters)`` fuses
-    the top-k page table into the same launch.
+    apply_scaling=False).  ``topk=(k, last_page, page_indices)`` also produces
+    the top-k page table (ekv_topk_pages semantics) in the same call.
     """
     require_gpu(q, k_min, k_max)
     B, H, _, D = q.shape
@@ -106,12 +106,12 @@ def estimate_page_criticality(q, k_min, k_max, alibi_slopes=None, q_pos: int = 0
     slopes = None
     if alibi_slopes is not None:
         slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
-    k_sel, last_page, pidx, counters = (-1, -1, None, None) if topk is None else topk
+    k_sel, last_page, pidx = (-1, -1, None) if topk is None else topk
     call("ekv_page_criticality", q3.data_ptr(), q3.stride(0), q3.stride(1),
          k_min.data_ptr(), k_max.data_ptr(), k_min.stride(0), k_min.stride(1), k_min.stride(2),
          ptr(slopes), out.data_ptr(), B, H, Hkv, D, num_pages, page_size, seq_len, q_pos,
          k_sel, last_page, ptr(pidx), 0 if pidx is None else pidx.stride(0),
-         0 if pidx is None else pidx.stride(1), ptr(counters), dtype_code(q.dtype),
+         0 if pidx is None else pidx.stride(1), dtype_code(q.dtype),
          stream_ptr(q.device))
     return out
 
@@ -162,8 +162,12 @@ def _cache_seqlens_2d(cache_seqlens, batch, num_kv_heads):
 def paged_entmax_decode(q, k_cache, v_cache, out, cache_seqlens, page_indices, page_size,
                         alpha, tau_mode: int, iters: int, tau: torch.Tensor | None,
                         alibi_slopes=None, q_seqlens=None, workspace: DecodeWorkspace | None = None,
-                        kv_rows: int | None = None):
-    """Shared launcher of the exact-tau (tau_mode 0) and given-tau (1) decode."""
+                        kv_rows: int | None = None, tau_in: torch.Tensor | None = None):
+    """Shared launcher of the exact-tau (tau_mode 0) and given-tau (1) decode.
+
+    The final tau goes to ``tau`` (the workspace's buffer when None); in
+    given-tau mode the start value is read from ``tau_in`` (default: ``tau``).
+    """
     require_gpu(q, k_cache, v_cache, out, page_indices)
     batch, nheads, q_len, dim = q.shape
     num_kv_heads = k_cache.shape[1]
@@ -192,6 +196,11 @@ def paged_entmax_decode(q, k_cache, v_cache, out, cache_seqlens, page_indices, p
         tau = workspace.taus
     assert tuple(tau.shape) == (batch, nheads) and tau.dtype == torch.float32 and tau.is_contiguous(), \
         "tau must be a contiguous float32 [B, H] tensor"
+    if tau_mode == 1:
+        if tau_in is None:
+            tau_in = tau
+        assert tuple(tau_in.shape) == (batch, nheads) and tau_in.dtype == torch.float32 \
+            and tau_in.is_contiguous(), "tau_in must be a contiguous float32 [B, H] tensor"
     q3 = _row_major_d(q[:, :, 0], "q")
     o3 = out[:, :, 0]
     direct = o3.stride(-1) == 1 and o3.data_ptr() % 16 == 0
@@ -209,7 +218,7 @@ def paged_entmax_decode(q, k_cache, v_cache, out, cache_seqlens, page_indices, p
          k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), kv_rows,
          page_indices.data_ptr(), page_indices.stride(0), page_indices.stride(1), n_slots,
          cache_seqlens.data_ptr(), cache_seqlens.stride(0), cache_seqlens.stride(1),
-         ptr(qsl), ptr(slopes), tau.data_ptr(), tau_mode, iters,
+         ptr(qsl), ptr(slopes), ptr(tau_in), tau.data_ptr(), tau_mode, iters,
          o_target.data_ptr(), o_target.stride(0), o_target.stride(1), float(alpha),
          qscale_for(alpha, dim, q.dtype), page_size, batch, nheads, num_kv_heads, dim,
          workspace.splits, workspace.max_tokens, workspace.buf.data_ptr(),

@@ -51,7 +51,6 @@ class PagedKVCache:
 
         self._page_indices_buf: Optional[torch.Tensor] = None
         self._page_indices_last_page: Optional[int] = None
-        self._topk_counters: Optional[torch.Tensor] = None
         self._scores_buf: Optional[torch.Tensor] = None
         self._paged_decode_workspaces: dict = {}
         self._gaussian_buffers: dict = {}
@@ -178,13 +177,10 @@ class PagedKVCache:
         self.last_page_scores = scores
         if k == 0:
             return buf
-        if self._topk_counters is None or self._topk_counters.numel() < B * Hkv \
-                or self._topk_counters.device != q.device:
-            self._topk_counters = torch.zeros(B * Hkv, dtype=torch.int32, device=q.device)
         K.estimate_page_criticality(
             q, self.k_min, self.k_max, alibi_slopes=alibi_slopes, q_pos=self.seq_len - 1,
             page_size=self.page_size, seq_len=self.seq_len, exclude_last_page=True,
-            out=scores, topk=(k, last, buf, self._topk_counters))
+            out=scores, topk=(k, last, buf))
         return buf
 
     def _get_scores_buf(self, B, H, P, dtype, device):

@@ -51,15 +51,13 @@ int ekv_append(const void* k_new, const void* v_new, int64_t new_stride_b, int64
  * sum_d max(q_d kmin_pd, q_d kmax_pd) (+ ALiBi bonus when alibi_slopes [H] is
  * non-null).  Replaces triton_estimate_page_criticality,
  * kernels/page_criticality.py:107-187.  When k_select >= 0 the top-k page
- * table is fused (see ekv_topk_pages) and `counters` ([B*Hkv] int32, zeroed
- * once) is required. */
+ * table of ekv_topk_pages is produced by the same call. */
 int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kmin,
                          const void* kmax, int64_t s_stride_b, int64_t s_stride_h,
                          int64_t s_stride_page, const float* alibi_slopes, void* scores, int B,
                          int H, int Hkv, int D, int num_pages, int page_size, int seq_len,
                          int q_pos, int k_select, int last_page, int32_t* page_indices,
-                         int64_t pi_stride_b, int64_t pi_stride_h, int32_t* counters, int dtype,
-                         void* stream);
+                         int64_t pi_stride_b, int64_t pi_stride_h, int dtype, void* stream);
 
 /* Top-k page table per (b, kv head): the k pages with the largest score (group
  * maximum under GQA), ascending, ties to the lower index, then `last_page`
@@ -75,8 +73,8 @@ int64_t ekv_decode_workspace_bytes(int B, int H, int Hkv, int D, int splits, int
 /* Paged alpha-entmax decode over the compacted page table (keyed by kv head).
  * tau_mode 0: exact (histogram init + `iters` bracketed Halley steps), the
  *   final tau is written to tau [B, H];
- * tau_mode 1: tau [B, H] holds the starting value; `iters` unbounded
- *   Halley/Newton corrections, final tau written back.
+ * tau_mode 1: tau_in [B, H] holds the starting value; `iters` unbounded
+ *   Halley/Newton corrections, final tau written to tau (may alias tau_in).
  * qscale = (alpha-1)/sqrt(D) rounded to the storage dtype.  kv_rows bounds
  * the rows addressable per (b, kv head); out-of-range page ids are skipped.
  * Replaces kernels/adadecode_paged.py:567-762 and
@@ -86,8 +84,8 @@ int ekv_paged_entmax_decode(const void* q, int64_t q_stride_b, int64_t q_stride_
                             int64_t kv_stride_row, int64_t kv_rows, const int32_t* page_indices,
                             int64_t pi_stride_b, int64_t pi_stride_h, int n_slots,
                             const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
-                            const int32_t* q_seqlens, const float* alibi_slopes, float* tau,
-                            int tau_mode, int iters, void* out, int64_t out_stride_b,
+                            const int32_t* q_seqlens, const float* alibi_slopes,
+                            const float* tau_in, float* tau, int tau_mode, int iters, void* out, int64_t out_stride_b,
                             int64_t out_stride_h, float alpha, float qscale, int page_size, int B,
                             int H, int Hkv, int D, int splits, int max_tokens, void* workspace,
                             int64_t workspace_bytes, int dtype, void* stream);

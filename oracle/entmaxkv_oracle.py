@@ -162,7 +162,8 @@ def topk_pages(scores: np.ndarray, k: int) -> np.ndarray:
     Follows attention_topk.py:52-55 (torch.topk over the page axis).  torch
     leaves the order among equal scores unspecified; this build fixes it:
     among equal scores the lower page index wins.  NaN ranks above every
-    number, as in torch.topk.
+    number and -0.0 ranks below +0.0, as in torch.topk's radix select on the
+    IEEE bit patterns.
     scores: [..., P]; returns int64 [..., k] sorted ascending.
     Pinned by: numpy lexsort brute force and torch.topk on tie-free rows.
     """
@@ -176,8 +177,9 @@ def topk_pages(scores: np.ndarray, k: int) -> np.ndarray:
         row = flat[r]
         key = np.where(np.isnan(row), np.inf, row)
         nanflag = np.isnan(row).astype(np.int64)
-        # sort by (nan first, value desc, index asc)
-        order = np.lexsort((idx, -key, -nanflag))
+        negzero = ((row == 0) & np.signbit(row)).astype(np.int64)
+        # sort by (nan first, value desc, +0.0 before -0.0, index asc)
+        order = np.lexsort((idx, negzero, -key, -nanflag))
         out[r] = np.sort(order[:k])
     return out.reshape(*lead, k)
 

@@ -53,6 +53,9 @@ def test_page_stats_initialize(dtype, S):
         assert g.shape == r.shape
         if name in ("min", "max"):
             np.testing.assert_array_equal(g, r)
+        elif dtype == "fp32":
+            # fp32 accumulation of <= 16 rows of O(1) values vs the float64 oracle
+            np.testing.assert_allclose(g, r, atol=2e-6, rtol=1e-6, err_msg=name)
         else:
             assert ulp_diff_16(g, r, dtype).max() <= 1.0, name
     np.testing.assert_array_equal(to_np(cache.k_cache), k)
@@ -97,10 +100,12 @@ def _build_cache(rng, B, Hkv, S, D, dtype, k_scale=1.0):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("G", [1, 4])
 @pytest.mark.parametrize("alibi", [False, True])
-def test_criticality_and_topk(dtype, G, alibi):
-    _case(test="criticality_topk", dtype=dtype, G=G, alibi=alibi)
+@pytest.mark.parametrize("path", ["split", "head"])
+def test_criticality_and_topk(dtype, G, alibi, path):
+    _case(test="criticality_topk", dtype=dtype, G=G, alibi=alibi, path=path)
     rng = np.random.default_rng(10 + G)
-    B, Hkv, S, D = 2, 2, 16 * 300 + 5, 128
+    B, Hkv = DECODE_SHAPES[path]
+    S, D = 16 * 300 + 5, 128
     H = Hkv * G
     cache, k, v = _build_cache(rng, B, Hkv, S, D, dtype)
     q = randn(rng, (B, H, 1, D), dtype)
@@ -116,7 +121,16 @@ def test_criticality_and_topk(dtype, G, alibi):
     ref_scores = O.page_criticality(q[:, :, 0], kmin, kmax, dtype, num_pages=P - 1,
                                     alibi_slopes=slopes, page_size=16, seq_len=S, q_pos=S - 1)
     got_scores = to_np(cache.last_page_scores)
-    assert ulp_diff_16(got_scores, ref_scores, dtype).max() <= 1.0
+    # fp32 accumulation (order differs from the float64 oracle) is exact to
+    # ~2^-20 of the magnitudes summed; the ALiBi bonus can cancel most of the
+    # score, so the bound is taken on the terms, then one rounding to the dtype.
+    plain = O.page_criticality(q[:, :, 0], kmin, kmax, "fp32", num_pages=P - 1)
+    terms = np.abs(plain)
+    if slopes is not None:
+        terms = terms + np.abs(O.alibi_page_bonus(slopes, P - 1, 16, S, S - 1))[None]
+    ulp = {"fp16": 2.0 ** -10, "bf16": 2.0 ** -7, "fp32": 2.0 ** -23}[dtype]
+    tol = 2.0 ** -20 * terms + ulp * np.abs(ref_scores)
+    assert (np.abs(got_scores - ref_scores) <= tol).all()
     # the page table is bit-exact given the scores the kernel produced
     group = O.topk_gqa_group_scores(got_scores, Hkv)
     ref_sel = O.topk_pages(group, kk)
@@ -160,15 +174,22 @@ def _decode_case(rng, dtype, B, Hkv, G, S, D, n_sel, k_scale=1.0):
     return K_, V_, q, pidx, seqlens
 
 
+# "split": few heads, scores from a separate many-workgroup launch;
+# "head": batch * kv heads >= 128, one workgroup per (b, kv head) end to end.
+DECODE_SHAPES = {"split": (2, 2), "head": (8, 16)}
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("alpha", [1.5, 2.0])
 @pytest.mark.parametrize("G", [1, 4])
 @pytest.mark.parametrize("niter", [2, 10])
-def test_decode_exact_matches_oracle(dtype, alpha, G, niter):
+@pytest.mark.parametrize("path", ["split", "head"])
+def test_decode_exact_matches_oracle(dtype, alpha, G, niter, path):
     K = _K()
-    _case(test="decode_exact", dtype=dtype, alpha=alpha, G=G, niter=niter)
+    _case(test="decode_exact", dtype=dtype, alpha=alpha, G=G, niter=niter, path=path)
     rng = np.random.default_rng(100 + G)
-    B, Hkv, S, D = 2, 2, 16 * 200 + 3, 128
+    B, Hkv = DECODE_SHAPES[path]
+    S, D = 16 * 200 + 3, 128
     Kc, Vc, q, pidx, seqlens = _decode_case(rng, dtype, B, Hkv, G, S, D, 64)
     H = Hkv * G
     dt = TORCH_DT[dtype]
@@ -182,7 +203,7 @@ def test_decode_exact_matches_oracle(dtype, alpha, G, niter):
     ref, ref_tau = O.paged_entmax_decode(q[:, :, 0], Kc, Vc, pidx, seqlens, 16, alpha, niter, dtype)
     assert_out_close(to_np(out)[:, :, 0], ref, dtype)
     np.testing.assert_allclose(to_np(taus), ref_tau, atol=1e-4)
-    if niter == 10:
+    if niter == 10 and path == "split":
         # converged: equals exact sort-based entmax over the selected tokens
         qs = O.scaled_query(q[:, :, 0], alpha, dtype)
         for b in range(B):
@@ -281,7 +302,10 @@ def test_topk_api_end_to_end(dtype, G):
     st = O.page_stats(Kf, ps, dtype)
     scores = to_np(cache.last_page_scores)
     ref_scores = O.page_criticality(q[:, :, 0], st[0], st[1], dtype, num_pages=P - 1)
-    assert ulp_diff_16(scores, ref_scores, dtype).max() <= 1.0
+    if dtype == "fp32":
+        np.testing.assert_allclose(scores, ref_scores, rtol=2e-6, atol=1e-4)
+    else:
+        assert ulp_diff_16(scores, ref_scores, dtype).max() <= 1.0
     sel = O.topk_pages(O.topk_gqa_group_scores(scores, Hkv), n_sel)
     pidx = np.concatenate([sel, np.full((B, Hkv, 1), P - 1)], axis=2)
     np.testing.assert_array_equal(to_np(cache._page_indices_buf).astype(np.int64), pidx)
@@ -329,8 +353,9 @@ def test_gaussian_stats_tau_select_clamp(dtype, alpha):
     torch.cuda.synchronize()
     P = cache.num_pages
     pfs = P - 1
-    kst = O.page_stats(k, ps, dtype)
-    ref = O.gaussian_page_stats(q[:, :, 0], kst[2], kst[3], pfs)
+    # the kernel is checked on the statistics the cache holds (those are pinned
+    # separately by test_page_stats_initialize)
+    ref = O.gaussian_page_stats(q[:, :, 0], to_np(cache.k_mean), to_np(cache.k_std), pfs)
     mu_p, sg_p = to_np(st["mu_scores_per_page"]), to_np(st["sigma_scores_per_page"])
     np.testing.assert_allclose(mu_p, ref["mu_p"], rtol=1e-5, atol=1e-5)
     np.testing.assert_allclose(sg_p, ref["sigma_p"], rtol=1e-5, atol=1e-6)

@@ -108,6 +108,11 @@ def test_topk_tie_rule_lower_index_wins():
     np.testing.assert_array_equal(O.topk_pages(s, 4), [[1, 2, 3, 4]])
     s2 = np.array([[1.0, np.nan, 5.0]])
     np.testing.assert_array_equal(O.topk_pages(s2, 1), [[1]])
+    # torch's radix select orders by IEEE bits: +0.0 above -0.0
+    s3 = np.array([[-0.0, -1.0, 0.0, -0.0]])
+    np.testing.assert_array_equal(O.topk_pages(s3, 1), [[2]])
+    t = torch.topk(torch.tensor(s3[0], dtype=torch.float16), 2).indices.tolist()
+    assert t[0] == 2
 
 
 # ---------------------------------------------------------------------------
