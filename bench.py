@@ -49,6 +49,9 @@ def _args():
     p.add_argument("--no-gaussian", action="store_true")
     p.add_argument("--only", choices=["topk", "gaussian", "criticality"], default=None,
                    help="run one step kind in a loop (for profilers)")
+    p.add_argument("--copy-calib-mib", type=int, default=0,
+                   help="with --only: first copy a buffer of this many MiB (a copy kernel of "
+                        "known traffic that scales rocprofv3's FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -131,6 +134,14 @@ def main():
     step_bytes = kv_bytes + crit_bytes + io_bytes
 
     if a.only:
+        if a.copy_calib_mib:
+            n = a.copy_calib_mib * (1 << 20) // 4
+            src = torch.ones(n, device=dev, dtype=torch.float32)
+            dst = torch.empty_like(src)
+            torch.cuda.synchronize()
+            dst.copy_(src)
+            torch.cuda.synchronize()
+            del src, dst
         fn = {"topk": topk_step, "criticality": crit_only}.get(a.only)
         if a.only == "gaussian":
             def fn():
@@ -148,7 +159,8 @@ def main():
     ms = ms_graph if ms_graph is not None else ms_eager
 
     # dominant kernel: criticality (+ fused top-k); average launch time over the timed loop
-    ms_crit = _time_loop(crit_only, a.steps, a.warmup, stream)
+    ms_crit = _time_loop(crit_only if a.no_graph else _graphed(crit_only, stream), a.steps,
+                         a.warmup, stream)
     crit_alg = crit_bytes + B * H * (P - 1) * esz  # bounds read + scores written
     crit_gbs = crit_alg / (ms_crit * 1e-3) / 1e9
 

@@ -9,7 +9,7 @@
 // and out = sum_c [s_c - tau]_+^(1/(alpha-1)) v_c (not renormalised, as in
 // the reference).
 //
-// One workgroup of 512 threads owns one (b, kv head) and all G query heads
+// One workgroup of 1024 threads owns one (b, kv head) and all G query heads
 // of its group, so nothing crosses workgroups:
 //   phase 1  stream the selected K rows once (16-byte loads, one load serves
 //            all G heads) and keep the fp32 scores in LDS (in the workspace
@@ -43,11 +43,14 @@ namespace {
 
 constexpr int kSplitThreads = 256;
 constexpr int kSplitUnroll = 4;
-constexpr int kHeadThreads = 512;
+constexpr int kHeadThreads = 1024;
 constexpr int kWaves = kHeadThreads / 64;
 constexpr int kBins = 16;
 constexpr int kBatch = 8;           // independent loads per lane in score passes
-constexpr int kWaveTauMax = 4096;   // longer token lists solve tau with the whole workgroup
+#ifndef EKV_WAVE_TAU_MAX
+#define EKV_WAVE_TAU_MAX 4096
+#endif
+constexpr int kWaveTauMax = EKV_WAVE_TAU_MAX;   // longer token lists solve tau with the whole workgroup
 constexpr int kHeadPathMinHeads = 128;
 constexpr int kTablePages = 2048;   // page ids staged in LDS per phase-1 chunk
 
@@ -570,7 +573,7 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
     }
     __syncthreads();
   }
-  EKV_STAMP(3);
+  EKV_STAMP(7);
 
   // reduce the row segments: within each wave by shuffles, then across waves
 #pragma unroll
@@ -715,7 +718,7 @@ extern "C" int ekv_paged_entmax_decode(
       constexpr int LPR = decltype(lpr)::value;
       return dispatch_group(G, [&](auto gv) {
         constexpr int GG = decltype(gv)::value;
-        constexpr int U = GG >= 4 ? 4 : 32 / GG;
+        constexpr int U = GG >= 4 ? 2 : 8 / GG;
         if (!head_path) {
           hipLaunchKernelGGL((score_split_kernel<T, LPR, GG>), dim3(splits, B * Hkv),
                              dim3(kSplitThreads), 0, s, a);
