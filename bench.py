@@ -210,15 +210,42 @@ def main():
                    "token_budget": a.budget, "selected_tokens_per_head": n_tok,
                    "alpha": a.alpha, "niter": a.niter, "timing": "hipGraph replay" if ms_graph else "eager",
                    "bytes_per_step": step_bytes},
-        "roofline": {"bound": "hbm", "kernel": "criticality_kernel (fused top-k)",
+        "roofline": {"bound": "hbm", "kernel": "criticality_head_kernel (fused top-k)",
                      "achieved": round(crit_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(crit_gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "avg_launch_us": round(ms_crit * 1e3, 2), "bytes_per_launch": crit_alg},
         "gaussian": gauss,
         "cpu_baseline": cpu,
     }
+    headline = (B, H, Hkv, D, L, a.budget, a.dtype) == (8, 32, 32, 128, 32768, 1024, "fp16")
+    traffic = _measured_traffic("criticality_head_kernel") if headline else None
+    if traffic:
+        line["roofline"]["traffic"] = traffic
+        line["roofline"]["frac_traffic"] = round(traffic / (ms_crit * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
     print(json.dumps(line), flush=True)
     return 0
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "criticality_head_kernel_pmc_b8h32l32k.md")
+
+
+def _measured_traffic(kernel_tag):
+    """HBM bytes per launch of the roofline kernel at the headline shape.
+
+    Read from the committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE,
+    each scaled by the factor a copy kernel of known size gives); None when
+    the summary is absent or was taken on another kernel build.
+    """
+    import re
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    k = re.search(r"^kernel:\s*(\S+)", text, re.M)
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
+    if not (k and m) or kernel_tag not in k.group(1):
+        return None
+    return int(m.group(1))
 
 
 def _cpu_baseline(a, esz):
@@ -237,15 +264,20 @@ def _cpu_baseline(a, esz):
     t0 = time.perf_counter()
     st = O.page_stats(k, ps, a.dtype)  # not timed as part of the step below
     t1 = time.perf_counter()
-    O.topk_decode_step(q, k, v, st, a.budget, ps, a.alpha, a.niter, a.dtype)
-    t2 = time.perf_counter()
+    reps = 0
+    while True:  # a bounded sample: repeat the step for about 10 s
+        O.topk_decode_step(q, k, v, st, a.budget, ps, a.alpha, a.niter, a.dtype)
+        reps += 1
+        if time.perf_counter() - t1 >= 10.0:
+            break
+    t2 = t1 + (time.perf_counter() - t1) / reps
     P = (S + ps - 1) // ps
     n_sel = min(a.budget // ps, P - 1)
     n_tok = n_sel * ps + (S - (P - 1) * ps)
     bytes_ = Hkv * n_tok * D * esz * 2 + H * (P - 1) * D * esz + 2 * H * D * esz
     return {"value": round(bytes_ / (t2 - t1) / 1e9, 4), "unit": "GB/s", "cores": 1,
             "kind": "port", "sample": f"one batch element (B=1, H={H}, L={S}) of the workload, "
-                                      f"NumPy float64 oracle, {t2 - t1:.2f} s per step",
+                                      f"NumPy float64 oracle, {reps} steps in ~10 s, {t2 - t1:.3f} s per step",
             "us_per_step": round((t2 - t1) * 1e6, 1)}
 
 

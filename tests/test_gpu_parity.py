@@ -214,6 +214,33 @@ def test_decode_exact_matches_oracle(dtype, alpha, G, niter, path):
                 assert_out_close(to_np(out)[b, h, 0], p @ Vc[b, h // G][rows], dtype, "exact")
 
 
+@pytest.mark.parametrize("n_sel", [400, 1699])
+def test_decode_long_heads(n_sel):
+    """One workgroup per head with long selections: 6405 tokens (block-wide tau
+    solve, scores staged in LDS) and 27189 tokens (scores in the workspace)."""
+    K = _K()
+    _case(test="decode_long", n_sel=n_sel)
+    rng = np.random.default_rng(31)
+    dtype = "fp16"
+    B, Hkv, S, D = 1, 128, 16 * 1700 + 5, 32
+    f16 = lambda *shape: rng.standard_normal(shape, dtype=np.float32).astype(np.float16).astype(np.float64)
+    Kc, Vc, q = f16(B, Hkv, S, D), f16(B, Hkv, S, D), f16(B, Hkv, 1, D)
+    P = (S + 15) // 16
+    pidx = np.stack([np.stack([np.concatenate([np.sort(rng.permutation(P - 1)[:n_sel]), [P - 1]])
+                               for _ in range(Hkv)]) for _ in range(B)])
+    seqlens = np.full((B, Hkv), n_sel * 16 + S - (P - 1) * 16)
+    out = torch.zeros(B, Hkv, 1, D, dtype=torch.float16, device="cuda")
+    taus = torch.zeros(B, Hkv, dtype=torch.float32, device="cuda")
+    K.sparse_attention_decode_paged(to_dev(q, dtype), to_dev(Kc, dtype), to_dev(Vc, dtype), out,
+                                    torch.tensor(seqlens, dtype=torch.int32, device="cuda"),
+                                    torch.tensor(pidx, dtype=torch.int32, device="cuda"), 16,
+                                    alpha=1.5, niter=2, taus_out=taus)
+    torch.cuda.synchronize()
+    ref, ref_tau = O.paged_entmax_decode(q[:, :, 0], Kc, Vc, pidx, seqlens, 16, 1.5, 2, dtype)
+    assert_out_close(to_np(out)[:, :, 0], ref, dtype)
+    np.testing.assert_allclose(to_np(taus), ref_tau, atol=1e-4)
+
+
 @pytest.mark.parametrize("dtype", ["fp16", "fp32"])
 @pytest.mark.parametrize("iters", [0, 1, 2])
 def test_decode_given_tau_matches_oracle(dtype, iters):
