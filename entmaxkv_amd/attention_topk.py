@@ -27,8 +27,9 @@ def sparse_attention_decode_paged(
 ):
     """Decode-phase attention with top-k page selection (attention_topk.py:8-100).
 
-    Launches: [append] -> criticality + top-k (one kernel) -> scores + tau ->
-    weighted sum.  ``cache_seqlens`` is the compacted token count supplied by the
+    Launches: [append] -> one kernel per (b, kv head) that scores every page,
+    selects the top-k pages and runs the exact-tau decode on them (two kernels
+    when a head does not fit one workgroup's LDS or the batch is small).  ``cache_seqlens`` is the compacted token count supplied by the
     caller, as in the reference (n_selected * page_size + last_page_size).
     ``splits`` and ``use_triton_criticality`` are accepted for compatibility.
     Under GQA the page table is per kv head (group maximum of page scores).
@@ -44,15 +45,27 @@ def sparse_attention_decode_paged(
     total_pages = (seq_len + page_size - 1) // page_size
     num_pages_to_select = min(token_budget // page_size, total_pages - 1)
 
-    page_indices = kv_cache.select_topk(q, num_pages_to_select, alibi_slopes=alibi_slopes)
-
     if workspace is None:
         workspace = kv_cache.get_paged_decode_workspace(
             batch, num_heads, head_dim, splits, 16, q.dtype, q.device,
             max_tokens=(num_pages_to_select + 1) * page_size)
 
-    K.paged_entmax_decode(
-        q, kv_cache._k, kv_cache._v, out, cache_seqlens, page_indices, page_size, alpha,
-        tau_mode=0, iters=niter, tau=None, alibi_slopes=alibi_slopes, q_seqlens=q_seqlens,
-        workspace=workspace, kv_rows=kv_cache.kv_capacity)
+    if num_pages_to_select == 0:
+        page_indices = kv_cache.select_topk(q, 0, alibi_slopes=alibi_slopes)
+        K.paged_entmax_decode(
+            q, kv_cache._k, kv_cache._v, out, cache_seqlens, page_indices, page_size, alpha,
+            tau_mode=0, iters=niter, tau=None, alibi_slopes=alibi_slopes, q_seqlens=q_seqlens,
+            workspace=workspace, kv_rows=kv_cache.kv_capacity)
+        return out
+
+    # criticality + top-k + decode in one launch (two when the shape needs it)
+    last = total_pages - 1
+    page_indices = kv_cache.get_page_indices_buf(batch, num_kv_heads, num_pages_to_select, last)
+    scores = kv_cache._get_scores_buf(batch, num_heads, total_pages - 1, q.dtype, q.device)
+    kv_cache.last_page_scores = scores
+    K.topk_paged_entmax_decode(
+        q, kv_cache.k_min, kv_cache.k_max, scores, num_pages_to_select, last, kv_cache._k,
+        kv_cache._v, out, page_indices, cache_seqlens, page_size, alpha, niter, seq_len,
+        seq_len - 1, alibi_slopes=alibi_slopes, q_seqlens=q_seqlens, workspace=workspace,
+        kv_rows=kv_cache.kv_capacity)
     return out

@@ -15,21 +15,32 @@
 // heads of the group.  When top-k is fused, the last workgroup of a
 // (b, kv head) to finish runs a block-wide radix select over the page scores
 // (already resident in L2) and writes the page table.
-#include "topk_device.h"
-#include "../../include/entmaxkv.h"
-
-using namespace ekv;
+#include "ekv_common.h"
 
 #ifdef EKV_PHASE_TIMERS
 __device__ unsigned long long ekv_crit_timers[4096 * 8];
+#define EKV_CSTAMP(i) \
+  if (threadIdx.x == 0 && blockIdx.x < 4096) ekv_crit_timers[blockIdx.x * 8 + (i)] = wall_clock64()
 extern "C" int ekv_debug_crit_timers(unsigned long long* host, int n) {
   return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(ekv_crit_timers), n * sizeof(unsigned long long));
 }
 #endif
 
+#include "topk_device.h"
+#include "../../include/entmaxkv.h"
+
+using namespace ekv;
+
 namespace {
 
 using namespace ekv::topk;
+
+// One workgroup of kHeadThreads per (b, kv head): scores every page of the
+// head (16-byte loads, kHeadUnroll pages per row segment in flight), keeps
+// the group-max keys in LDS and, when k_sel >= 0, selects the top-k pages in
+// the same workgroup.  No cross-workgroup communication.
+constexpr int kHeadThreads = 512;
+constexpr int kHeadUnroll = 8;
 
 template <typename T, int LPR, int G, int U>
 __global__ __launch_bounds__(kHeadThreads) void criticality_head_kernel(
@@ -38,68 +49,20 @@ __global__ __launch_bounds__(kHeadThreads) void criticality_head_kernel(
     const float* __restrict__ slopes, T* __restrict__ scores, int H, int Hkv, int num_pages,
     int page_size, int seq_len, int q_pos, int k_sel, int last_page, int32_t* page_indices,
     int64_t pisb, int64_t pish, int lds_key_cap) {
-  constexpr int VEC = 16 / sizeof(T);
-  constexpr int SEGS = kHeadThreads / LPR;
-  constexpr int ROUND = SEGS * U;
   extern __shared__ uint32_t lds_keys[];
-  const int seg = threadIdx.x / LPR;
-  const int sl = threadIdx.x % LPR;
-  const int col = sl * VEC;
   const int bkv = blockIdx.x;
   const int b = bkv / Hkv, kvh = bkv % Hkv;
-  const int h0 = kvh * G;
   const bool keep_keys = k_sel >= 0 && num_pages <= lds_key_cap;
   EKV_CSTAMP(0);
-
-  // q in its storage format plus a per-element "q >= 0" mask: the bound of
-  // element d is kmax where q_d >= 0 and kmin elsewhere (kernels/page_criticality.py:88-95)
-  uint4 qraw[G], qmask[G];
-  float slope[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    qraw[g] = ld16(q + b * qsb + (h0 + g) * qsh + col);
-    qmask[g] = Dot16<T>::nonneg_mask(qraw[g]);
-    slope[g] = slopes ? slopes[h0 + g] : 0.f;
-  }
-  const T* kmn = kmin + b * ssb + kvh * ssh;
-  const T* kmx = kmax + b * ssb + kvh * ssh;
-  T* sbase = scores + ((int64_t)b * H + h0) * num_pages;
-
-  for (int p0 = 0; p0 < num_pages; p0 += ROUND) {
-    uint4 lo[U], hi[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int p = p0 + u * SEGS + seg;
-      if (p < num_pages) {
-        lo[u] = ld16(kmn + (int64_t)p * ssp + col);
-        hi[u] = ld16(kmx + (int64_t)p * ssp + col);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int p = p0 + u * SEGS + seg;
-      uint32_t key = 0;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float acc = Dot16<T>::dot(qraw[g], bit_select(lo[u], hi[u], qmask[g]), 0.f);
-        acc = seg_sum<LPR>(acc);
-        if (slopes) {
-          const int last_pos = min((p + 1) * page_size - 1, seq_len - 1);
-          acc = add_rn(acc, mul_rn(slope[g], (float)(last_pos - q_pos)));
-        }
-        const T sv = from_f<T>(acc);
-        key = max(key, ScoreKey<T>::key(sv));
-        if (p < num_pages && sl == 0) sbase[(int64_t)g * num_pages + p] = sv;
-      }
-      if (keep_keys && p < num_pages && sl == 0) lds_keys[p] = key;
-    }
-  }
+  T* sbase = criticality_scan_head<T, LPR, G, kHeadThreads, U>(
+      q, qsb, qsh, kmin, kmax, ssb, ssh, ssp, slopes, scores, H, num_pages, page_size, seq_len,
+      q_pos, b, kvh, keep_keys ? lds_keys : nullptr);
   if (k_sel < 0) return;
   __syncthreads();
   EKV_CSTAMP(1);
   topk_select_block<T, G, kHeadThreads>(sbase, num_pages, num_pages, k_sel, last_page,
-                                               page_indices + b * pisb + kvh * pish, lds_keys,
-                                               keep_keys ? num_pages : 0, keep_keys);
+                                        page_indices + b * pisb + kvh * pish, lds_keys,
+                                        keep_keys ? num_pages : 0, keep_keys);
 }
 
 template <typename T, int LPR, int G>

@@ -157,36 +157,117 @@ __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<
 // wave-level reductions (wave64)
 // ---------------------------------------------------------------------------
 
+// Lane exchanges without the LDS crossbar: DPP within a row of 16 lanes and
+// the gfx950 permlane swaps across rows (v_permlane16_swap_b32 exchanges the
+// odd rows of one register with the even rows of another, v_permlane32_swap_b32
+// the upper half with the lower half; applied to two copies of one value, the
+// two results hold the value of lane i and of lane i ^ 16 (resp. ^ 32)).
+namespace lanes {
+// DPP controls (GCN/CDNA encoding)
+constexpr int kQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141;  // lane i <- 7 - i within 8
+constexpr int kRowMirror = 0x140;      // lane i <- 15 - i within 16
+constexpr int kRowRor4 = 0x124;        // lane i <- (i + 4) % 16 within 16
+constexpr int kRowRor8 = 0x128;        // lane i <- (i + 8) % 16 within 16
+
+template <int CTRL> __device__ __forceinline__ uint32_t dpp(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+// (value of lane i, value of lane i ^ 16)
+__device__ __forceinline__ void swap16(uint32_t x, uint32_t& a, uint32_t& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  a = r[0];
+  b = r[1];
+}
+__device__ __forceinline__ void swap32(uint32_t x, uint32_t& a, uint32_t& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  a = r[0];
+  b = r[1];
+}
+
+struct Add {
+  template <typename V> __device__ __forceinline__ V operator()(V a, V b) const { return a + b; }
+};
+struct Max {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+  __device__ __forceinline__ int operator()(int a, int b) const { return a > b ? a : b; }
+};
+
+template <typename V> __device__ __forceinline__ uint32_t bits(V x) {
+  return __builtin_bit_cast(uint32_t, x);
+}
+template <typename V> __device__ __forceinline__ V from_bits(uint32_t x) {
+  return __builtin_bit_cast(V, x);
+}
+
+// All-reduce over aligned segments of L lanes (L a power of two <= 64).
+template <int L, typename V, typename Op>
+__device__ __forceinline__ V seg_reduce(V x, Op op) {
+  if constexpr (L >= 2) x = op(x, from_bits<V>(dpp<kQuadXor1>(bits(x))));
+  if constexpr (L >= 4) x = op(x, from_bits<V>(dpp<kQuadXor2>(bits(x))));
+  if constexpr (L >= 8) x = op(x, from_bits<V>(dpp<kRowHalfMirror>(bits(x))));
+  if constexpr (L >= 16) x = op(x, from_bits<V>(dpp<kRowMirror>(bits(x))));
+  if constexpr (L >= 32) {
+    uint32_t a, b;
+    swap16(bits(x), a, b);
+    x = op(from_bits<V>(a), from_bits<V>(b));
+  }
+  if constexpr (L >= 64) {
+    uint32_t a, b;
+    swap32(bits(x), a, b);
+    x = op(from_bits<V>(a), from_bits<V>(b));
+  }
+  return x;
+}
+
+// Sum over the lanes of a wave that share the same position within their
+// segment of L lanes (lane i and every lane i ^ (m * L)); every lane receives
+// the sum of its position.
+template <int L>
+__device__ __forceinline__ float cross_seg_sum(float x) {
+  if constexpr (L <= 4) x += from_bits<float>(dpp<kRowRor8>(bits(x)));
+  if constexpr (L <= 4) x += from_bits<float>(dpp<kRowRor4>(bits(x)));
+  if constexpr (L == 8) x += from_bits<float>(dpp<kRowRor8>(bits(x)));
+  if constexpr (L <= 16) {
+    uint32_t a, b;
+    swap16(bits(x), a, b);
+    x = from_bits<float>(a) + from_bits<float>(b);
+  }
+  if constexpr (L <= 32) {
+    uint32_t a, b;
+    swap32(bits(x), a, b);
+    x = from_bits<float>(a) + from_bits<float>(b);
+  }
+  return x;
+}
+}  // namespace lanes
+
 // Sum over an aligned segment of L lanes (L a power of two <= 64); every lane
 // of the segment receives the result.
 template <int L> __device__ __forceinline__ float seg_sum(float x) {
-#pragma unroll
-  for (int o = L / 2; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-  return x;
+  return lanes::seg_reduce<L>(x, lanes::Add{});
 }
 
 __device__ __forceinline__ float wave_sum(float x) { return seg_sum<64>(x); }
 
 __device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
-  return x;
+  return lanes::seg_reduce<64>(x, lanes::Max{});
 }
 
-__device__ __forceinline__ int wave_sum_i(int x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-  return x;
-}
+__device__ __forceinline__ int wave_sum_i(int x) { return lanes::seg_reduce<64>(x, lanes::Add{}); }
 
-// Inclusive prefix sum over the 64 lanes of a wave.
+// Inclusive prefix sum over the 64 lanes of a wave: Hillis-Steele steps
+// within each row of 16 lanes (DPP row_shr), then the row totals carried
+// across rows (DPP row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2
+// and 3).  Lanes without a source read 0.
 __device__ __forceinline__ int wave_incl_scan(int x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
   return x;
 }
 

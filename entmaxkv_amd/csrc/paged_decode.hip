@@ -23,6 +23,7 @@
 // and the head kernel starts at phase 2.  The reference launches 7 + 2*niter
 // kernels and reads K 3 + niter times.
 #include "ekv_common.h"
+#include "topk_device.h"
 #include "../../include/entmaxkv.h"
 
 using namespace ekv;
@@ -35,8 +36,15 @@ __device__ unsigned long long ekv_phase_timers[4096 * 8];
 extern "C" int ekv_debug_phase_timers(unsigned long long* host, int n) {
   return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(ekv_phase_timers), n * sizeof(unsigned long long));
 }
+__device__ unsigned long long ekv_fused_timers[4096 * 4];
+#define EKV_FSTAMP(i) \
+  if (threadIdx.x == 0 && blockIdx.x < 4096) ekv_fused_timers[blockIdx.x * 4 + (i)] = wall_clock64()
+extern "C" int ekv_debug_fused_timers(unsigned long long* host, int n) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(ekv_fused_timers), n * sizeof(unsigned long long));
+}
 #else
 #define EKV_STAMP(i)
+#define EKV_FSTAMP(i)
 #endif
 
 namespace {
@@ -195,10 +203,24 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
 __device__ __forceinline__ void histogram_init(const int* hist, float gmax, float alpha, float& t, float& t_lo,
                                float& t_hi) {
   const float t0 = gmax - 1.0f;
+  // all bins in registers first (one LDS round trip instead of one per bin)
+  int hv[kBins];
+  {
+    const int4* h4 = reinterpret_cast<const int4*>(hist);
+#pragma unroll
+    for (int j = 0; j < kBins / 4; ++j) {
+      const int4 x = h4[j];
+      hv[4 * j] = x.x;
+      hv[4 * j + 1] = x.y;
+      hv[4 * j + 2] = x.z;
+      hv[4 * j + 3] = x.w;
+    }
+  }
   if (alpha == 2.0f || alpha == 1.5f) {
     float sum_z = 1.f, sum_k = 1.f, sum_z2 = 1.f;
+#pragma unroll
     for (int sj = kBins - 1; sj >= 0; --sj) {
-      float c_bin = (float)hist[sj];
+      float c_bin = (float)hv[sj];
       if (sj == kBins - 1) c_bin -= 1.0f;
       const float c_tau = (float)sj / (float)kBins;
       const float new_z = sum_z + c_bin * c_tau;
@@ -232,10 +254,11 @@ __device__ __forceinline__ void histogram_init(const int* hist, float gmax, floa
     for (int it = 0; it < 5; ++it) {
       const int mid = (int)((float)(lo + hi) * 0.5f);
       float fL = 0.f, fU = 0.f;
+#pragma unroll
       for (int j = 0; j < kBins; ++j) {
         const int off = j - mid;
         if (off < 0) continue;
-        float cnt = (float)hist[j];
+        float cnt = (float)hv[j];
         if (j == kBins - 1) cnt -= 1.0f;
         const float zL = (float)off / kBins;
         const float zU = ((float)off + 1.0f) / kBins;
@@ -288,46 +311,76 @@ __device__ __forceinline__ float halley_unbounded(float t, float a0, float a1, f
   return tn;
 }
 
-// Reduction scope of a tau solve: one wave (lanes stride 64) or the whole
-// workgroup (threads stride NT, block reductions through LDS).
-struct WaveScope {
-  static __device__ __forceinline__ int first() { return threadIdx.x & 63; }
-  static constexpr int kStride = 64;
-  static __device__ __forceinline__ float sum(float x, float*) { return wave_sum(x); }
-  static __device__ __forceinline__ float max(float x, float*) { return wave_max(x); }
-  static __device__ __forceinline__ void sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+// Reduction scope of a tau solve: a team of W consecutive waves owns one head
+// (lanes stride 64 * W).  W = 1 needs no workgroup barrier; for W > 1 every
+// wave of the workgroup makes the same sequence of reductions (a wave without
+// a head runs the solve on zero scores), and the partials of each reduction
+// go through one of two LDS buffers in turn, so one barrier per reduction
+// suffices.
+template <int W>
+struct TeamScope {
+  static constexpr int kStride = 64 * W;
+  float4* part;  // [2][kWaves] per-wave partials (LDS)
+  int wid, lane, team, pos, parity;
+  __device__ __forceinline__ TeamScope(float4* p) : part(p), parity(0) {
+    wid = threadIdx.x >> 6;
+    lane = threadIdx.x & 63;
+    team = wid / W;
+    pos = wid % W;
   }
-};
-
-template <int NT>
-struct BlockScope {
-  static __device__ __forceinline__ int first() { return threadIdx.x; }
-  static constexpr int kStride = NT;
-  static __device__ __forceinline__ float sum(float x, float* scratch) {
-    return block_sum(x, scratch);
+  __device__ __forceinline__ int first() const { return pos * 64 + lane; }
+  __device__ __forceinline__ void sync() const {
+    if constexpr (W == 1) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    } else {
+      __syncthreads();
+    }
   }
-  static __device__ __forceinline__ float max(float x, float* scratch) {
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  __device__ __forceinline__ float max(float x) {
     x = wave_max(x);
-    if (lane == 0) scratch[wid] = x;
-    __syncthreads();
-    float r = -INFINITY;
-    for (int w = 0; w < NT / 64; ++w) r = fmaxf(r, scratch[w]);
-    __syncthreads();
-    return r;
+    if constexpr (W > 1) {
+      float4* buf = part + parity * kWaves;
+      if (lane == 0) buf[wid].x = x;
+      __syncthreads();
+      x = buf[team * W].x;
+#pragma unroll
+      for (int w = 1; w < W; ++w) x = fmaxf(x, buf[team * W + w].x);
+      parity ^= 1;
+    }
+    return x;
   }
-  static __device__ __forceinline__ void sync() { __syncthreads(); }
+  __device__ __forceinline__ void sum3(float& a, float& b, float& c) {
+    a = wave_sum(a);
+    b = wave_sum(b);
+    c = wave_sum(c);
+    if constexpr (W > 1) {
+      float4* buf = part + parity * kWaves;
+      if (lane == 0) buf[wid] = make_float4(a, b, c, 0.f);
+      __syncthreads();
+      float4 r = buf[team * W];
+#pragma unroll
+      for (int w = 1; w < W; ++w) {
+        const float4 y = buf[team * W + w];
+        r.x += y.x;
+        r.y += y.y;
+        r.z += y.z;
+      }
+      a = r.x;
+      b = r.y;
+      c = r.z;
+      parity ^= 1;
+    }
+  }
 };
 
 // One pass over scores[0..n) of a head: the sums of [s - t]_+^(1/(alpha-1) - j)
 // for j = 0, 1, 2 (kernels/adadecode_paged.py:357-372), branch-free per score.
 template <typename S>
-__device__ __forceinline__ void accumulate_pass(const float* __restrict__ sc, int n, float t,
-                                                float alpha, float c0, float* scratch, float& a0,
-                                                float& a1, float& a2) {
+__device__ __forceinline__ void accumulate_pass(S& sp, const float* __restrict__ sc, int n, float t,
+                                                float alpha, float c0, float& a0, float& a1,
+                                                float& a2) {
   float s0 = 0.f, s1 = 0.f, s2 = 0.f;
   const bool generic = !(alpha == 2.0f || alpha == 1.5f);
   const bool sparsemax = alpha == 2.0f;
@@ -335,7 +388,7 @@ __device__ __forceinline__ void accumulate_pass(const float* __restrict__ sc, in
     float x[kBatch];
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
-      const int c = b0 + j * S::kStride + S::first();
+      const int c = b0 + j * S::kStride + sp.first();
       x[j] = c < n ? sc[c] : -INFINITY;
     }
     if (!generic) {
@@ -360,14 +413,18 @@ __device__ __forceinline__ void accumulate_pass(const float* __restrict__ sc, in
       }
     }
   }
-  a0 = S::sum(s0, scratch);
-  a1 = S::sum(s1, scratch);
-  a2 = S::sum(s2, scratch);
+  sp.sum3(s0, s1, s2);
+  a0 = s0;
+  a1 = s1;
+  a2 = s2;
 }
 
+// tau of one head (kernels/adadecode_paged.py:140-247, 357-372 and
+// kernels/adadecode_paged_gaussian_tau.py:12-53).  `hist` (kBins ints, LDS)
+// must be zero on entry when tau_mode is 0.
 template <typename S>
-__device__ __forceinline__ float solve_tau(const DecodeArgs& a, const float* __restrict__ sc,
-                                           int n, float tau_in, int* hist, float* scratch) {
+__device__ __forceinline__ float solve_tau(S& sp, const DecodeArgs& a, const float* __restrict__ sc,
+                                           int n, float tau_in, int* hist) {
   const float alpha = a.alpha;
   const float c0 = 1.0f / (alpha - 1.0f);
   const float c1 = c0 - 1.0f;
@@ -377,39 +434,37 @@ __device__ __forceinline__ float solve_tau(const DecodeArgs& a, const float* __r
     for (int b0 = 0; b0 < n; b0 += S::kStride * kBatch) {
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
-        const int c = b0 + j * S::kStride + S::first();
+        const int c = b0 + j * S::kStride + sp.first();
         if (c < n) m = fmaxf(m, sc[c]);
       }
     }
-    const float gmax = S::max(m, scratch);
+    const float gmax = sp.max(m);
     EKV_STAMP(4);
     const float t0 = gmax - 1.0f;
-    if (S::first() < kBins) hist[S::first()] = 0;
-    S::sync();
     for (int b0 = 0; b0 < n; b0 += S::kStride * kBatch) {
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
-        const int c = b0 + j * S::kStride + S::first();
+        const int c = b0 + j * S::kStride + sp.first();
         if (c < n) {
           const float f = (sc[c] - t0) * (float)kBins;
           if (f > -1.0f) atomicAdd(&hist[min((int)f, kBins - 1)], 1);
         }
       }
     }
-    S::sync();
+    sp.sync();
     float t_lo, t_hi;
     EKV_STAMP(5);
     histogram_init(hist, gmax, alpha, t, t_lo, t_hi);
     for (int it = 0; it < a.iters; ++it) {
       float a0, a1, a2;
-      accumulate_pass<S>(sc, n, t, alpha, c0, scratch, a0, a1, a2);
+      accumulate_pass(sp, sc, n, t, alpha, c0, a0, a1, a2);
       halley_bisect(t, t_lo, t_hi, a0, a1, a2, c0, c1);
     }
   } else {
     t = tau_in;
     for (int it = 0; it < a.iters; ++it) {
       float a0, a1, a2;
-      accumulate_pass<S>(sc, n, t, alpha, c0, scratch, a0, a1, a2);
+      accumulate_pass(sp, sc, n, t, alpha, c0, a0, a1, a2);
       t = halley_unbounded(t, a0, a1, a2, c0, c1);
     }
   }
@@ -442,7 +497,7 @@ __global__ __launch_bounds__(kSplitThreads) void score_split_kernel(DecodeArgs a
 
 struct HeadShared {
   int (*hist)[kBins];
-  float* scratch;
+  float4* part;  // [2][kWaves] reduction partials
   float* s_tau;
   int64_t* sup_row;
   float* sup_p;  // [G][kHeadThreads]
@@ -451,9 +506,25 @@ struct HeadShared {
   int* s_pages;  // [kTablePages]
 };
 
+// tau of the G heads of one (b, kv head): head g is solved by the team of W
+// waves g * W .. g * W + W - 1 (short token lists: W = 4 / G, one wave per
+// SIMD; long ones: every wave of the workgroup).
+template <int W, int G>
+__device__ __forceinline__ void solve_heads(const DecodeArgs& a, int b, int h0, int n,
+                                            const float* sc, int64_t stride,
+                                            const HeadShared& sh) {
+  TeamScope<W> sp(sh.part);
+  const int g = sp.team;
+  if (W == 1 && g >= G) return;
+  const bool real = g < G;
+  const float tin = (real && a.tau_mode == 1) ? a.tau_in[b * a.H + h0 + g] : 0.f;
+  const float t = solve_tau(sp, a, sc + (real ? g : 0) * stride, real ? n : 0, tin, sh.hist[g]);
+  if (real && sp.pos == 0 && sp.lane == 0) sh.s_tau[g] = t;
+}
+
 // Phases 1-3 of one (b, kv head); `sc` points to LDS when kStaged (so every
 // score access is a ds_* instruction) and to the workspace otherwise.
-template <typename T, int LPR, int G, int U, bool kStaged>
+template <typename T, int LPR, int G, int U, bool kStaged, bool kTableInLds = false>
 __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int kvh, int n,
                                                  float* sc, int64_t stride, const HeadShared& sh) {
   constexpr int VEC = 16 / sizeof(T);
@@ -466,8 +537,12 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
   const int32_t* pi = a.page_indices + b * a.pisb + kvh * a.pish;
 
   EKV_STAMP(0);
+  if (tid < kWaves * kBins) (&sh.hist[0][0])[tid] = 0;  // read after the phase-1 barriers
   // phase 1: scores, the page table staged in LDS chunk by chunk
-  if (!a.scores_ready) {
+  if (kTableInLds) {
+    // the whole page table is already in sh.s_pages (written by this workgroup)
+    score_rows<T, LPR, G, kHeadThreads, U>(a, b, kvh, 0, n, sc, stride, sh.s_pages, 0);
+  } else if (!a.scores_ready) {
     for (int cb = 0; cb < n; cb += kTablePages * ps) {
       const int ce = min(n, cb + kTablePages * ps);
       const int np = (ce - cb + ps - 1) / ps;
@@ -481,21 +556,11 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
   __syncthreads();
   EKV_STAMP(3);
 
-  // phase 2: tau per head
+  // phase 2: tau per head, one team of waves per head
   if (n <= kWaveTauMax) {
-    for (int g = wid; g < G; g += kWaves) {
-      const float tin = a.tau_mode == 1 ? a.tau_in[b * a.H + h0 + g] : 0.f;
-      const float t = solve_tau<WaveScope>(a, sc + g * stride, n, tin, sh.hist[wid], nullptr);
-      if (lane == 0) sh.s_tau[g] = t;
-    }
+    solve_heads<(G >= 4 ? 1 : 4 / G), G>(a, b, h0, n, sc, stride, sh);
   } else {
-    for (int g = 0; g < G; ++g) {
-      const float tin = a.tau_mode == 1 ? a.tau_in[b * a.H + h0 + g] : 0.f;
-      const float t = solve_tau<BlockScope<kHeadThreads>>(a, sc + g * stride, n, tin, sh.hist[0],
-                                                          sh.scratch);
-      if (tid == 0) sh.s_tau[g] = t;
-      __syncthreads();
-    }
+    solve_heads<kWaves / G, G>(a, b, h0, n, sc, stride, sh);
   }
   __syncthreads();
   float tau[G];
@@ -532,7 +597,7 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
         }
       }
       if (any) {
-        row = token_row(pi, c, ps, a.row_limit);
+        row = token_row(kTableInLds ? sh.s_pages : pi, c, ps, a.row_limit);
         if (row < 0) any = false;
       }
     }
@@ -580,10 +645,7 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
   for (int g = 0; g < G; ++g) {
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
-      float x = acc[g][i];
-#pragma unroll
-      for (int o = LPR; o < 64; o <<= 1) x += __shfl_xor(x, o, 64);
-      acc[g][i] = x;
+      acc[g][i] = lanes::cross_seg_sum<LPR>(acc[g][i]);
     }
     if (lane < LPR) {
 #pragma unroll
@@ -606,15 +668,15 @@ __global__ __launch_bounds__(kHeadThreads) void decode_head_kernel(DecodeArgs a)
   constexpr int VEC = 16 / sizeof(T);
   constexpr int D = LPR * VEC;
   extern __shared__ float stage[];  // [G][stage_cap] scores when staged
-  __shared__ int hist[kWaves][kBins];
-  __shared__ float scratch[kWaves + 1];
+  __shared__ __attribute__((aligned(16))) int hist[kWaves][kBins];
+  __shared__ float4 part[2 * kWaves];
   __shared__ float s_tau[G];
   __shared__ int64_t sup_row[kHeadThreads];
   __shared__ float sup_p[G * kHeadThreads];
   __shared__ int flag_cnt[kWaves];
   __shared__ float red[kWaves * D];
   __shared__ int s_pages[kTablePages];
-  const HeadShared sh{hist, scratch, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
+  const HeadShared sh{hist, part, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
 
   const int bkv = blockIdx.x;
   const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
@@ -627,6 +689,59 @@ __global__ __launch_bounds__(kHeadThreads) void decode_head_kernel(DecodeArgs a)
   }
 }
 
+// Criticality scan + top-k page selection of one step, as read by the fused
+// kernel (see ekv_topk_paged_entmax_decode).
+struct SelectArgs {
+  const void* kmin;
+  const void* kmax;
+  int64_t ssb, ssh, ssp;
+  void* scores;       // [B, H, num_pages] query dtype
+  int num_pages;      // pages scored (the last, partial page excluded)
+  int seq_len, q_pos;
+  int k;              // pages selected per (b, kv head)
+  int last_page;      // appended at slot k (the sentinel), or -1
+  int key_cap;        // page keys that fit the dynamic LDS
+};
+
+// One (b, kv head) per workgroup end to end: criticality scan of every page,
+// top-k (page table to global memory and to LDS), then phases 1-3 of the
+// decode on the selected pages.  Keys and then scores share the dynamic LDS.
+template <typename T, int LPR, int G, int UC, int UD>
+__global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a, SelectArgs t) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int D = LPR * VEC;
+  extern __shared__ float stage[];
+  __shared__ __attribute__((aligned(16))) int hist[kWaves][kBins];
+  __shared__ float4 part[2 * kWaves];
+  __shared__ float s_tau[G];
+  __shared__ int64_t sup_row[kHeadThreads];
+  __shared__ float sup_p[G * kHeadThreads];
+  __shared__ int flag_cnt[kWaves];
+  __shared__ float red[kWaves * D];
+  __shared__ int s_pages[kTablePages];
+  const HeadShared sh{hist, part, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
+
+  const int bkv = blockIdx.x;
+  const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
+  uint32_t* keys = reinterpret_cast<uint32_t*>(stage);
+  const bool keep = t.num_pages <= t.key_cap;
+  EKV_FSTAMP(0);
+  const T* sbase = topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC>(
+      (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
+      a.slopes, (T*)t.scores, a.H, t.num_pages, a.page_size, t.seq_len, t.q_pos, b, kvh,
+      keep ? keys : nullptr);
+  __syncthreads();
+  EKV_FSTAMP(1);
+  int32_t* pi = const_cast<int32_t*>(a.page_indices) + b * a.pisb + kvh * a.pish;
+  topk::topk_select_block<T, G, kHeadThreads>(sbase, t.num_pages, t.num_pages, t.k, t.last_page,
+                                              pi, keys, keep ? t.num_pages : 0, keep, s_pages);
+  __syncthreads();
+  EKV_FSTAMP(2);
+  const int n = token_count(a, b, kvh);
+  decode_head_body<T, LPR, G, UD, true, true>(a, b, kvh, n, stage, a.stage_cap, sh);
+  EKV_FSTAMP(3);
+}
+
 template <typename F>
 int dispatch_group(int G, F&& f) {
   switch (G) {
@@ -636,6 +751,51 @@ int dispatch_group(int G, F&& f) {
     case 8: return f(std::integral_constant<int, 8>{});
     default: return set_error(EKV_ERR_ARG, "GQA group size %d unsupported (1, 2, 4 or 8)", G);
   }
+}
+
+DecodeArgs make_decode_args(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k, const void* v,
+    int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+    const int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h, int n_slots,
+    const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
+    const int32_t* q_seqlens, const float* alibi_slopes, const float* tau_in, float* tau,
+    int tau_mode, int iters, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha,
+    float qscale, int page_size, int H, int Hkv, int splits, int max_tokens, void* workspace) {
+  DecodeArgs a;
+  a.q = q;
+  a.qsb = q_stride_b;
+  a.qsh = q_stride_h;
+  a.k = k;
+  a.v = v;
+  a.ksb = kv_stride_b;
+  a.ksh = kv_stride_h;
+  a.ksr = kv_stride_row;
+  a.row_limit = kv_rows;
+  a.page_indices = page_indices;
+  a.pisb = pi_stride_b;
+  a.pish = pi_stride_h;
+  a.n_slots = n_slots;
+  a.cache_seqlens = cache_seqlens;
+  a.csb = cs_stride_b;
+  a.csh = cs_stride_h;
+  a.q_seqlens = q_seqlens;
+  a.slopes = alibi_slopes;
+  a.tau = tau;
+  a.tau_in = tau_in;
+  a.tau_mode = tau_mode;
+  a.iters = iters;
+  a.out = out;
+  a.osb = out_stride_b;
+  a.osh = out_stride_h;
+  a.alpha = alpha;
+  a.qscale = qscale;
+  a.page_size = page_size;
+  a.H = H;
+  a.Hkv = Hkv;
+  a.splits = splits;
+  a.max_tokens = max_tokens;
+  a.ws_scores = (float*)workspace;
+  return a;
 }
 
 // LDS per workgroup on gfx950, and the part of it given to staged scores.
@@ -672,40 +832,12 @@ extern "C" int ekv_paged_entmax_decode(
   EKV_REQUIRE(alpha > 1.0f, "ekv_paged_entmax_decode: alpha must be > 1");
   EKV_REQUIRE(workspace_bytes >= ekv_decode_workspace_bytes(B, H, Hkv, D, splits, max_tokens),
               "ekv_paged_entmax_decode: workspace too small");
-  DecodeArgs a;
-  a.q = q;
-  a.qsb = q_stride_b;
-  a.qsh = q_stride_h;
-  a.k = k;
-  a.v = v;
-  a.ksb = kv_stride_b;
-  a.ksh = kv_stride_h;
-  a.ksr = kv_stride_row;
-  a.row_limit = kv_rows;
-  a.page_indices = page_indices;
-  a.pisb = pi_stride_b;
-  a.pish = pi_stride_h;
-  a.n_slots = n_slots;
-  a.cache_seqlens = cache_seqlens;
-  a.csb = cs_stride_b;
-  a.csh = cs_stride_h;
-  a.q_seqlens = q_seqlens;
-  a.slopes = alibi_slopes;
-  a.tau = tau;
-  a.tau_in = tau_in;
-  a.tau_mode = tau_mode;
-  a.iters = iters;
-  a.out = out;
-  a.osb = out_stride_b;
-  a.osh = out_stride_h;
-  a.alpha = alpha;
-  a.qscale = qscale;
-  a.page_size = page_size;
-  a.H = H;
-  a.Hkv = Hkv;
-  a.splits = splits;
-  a.max_tokens = max_tokens;
-  a.ws_scores = (float*)workspace;
+  DecodeArgs a = make_decode_args(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h,
+                                  kv_stride_row, kv_rows, page_indices, pi_stride_b, pi_stride_h,
+                                  n_slots, cache_seqlens, cs_stride_b, cs_stride_h, q_seqlens,
+                                  alibi_slopes, tau_in, tau, tau_mode, iters, out, out_stride_b,
+                                  out_stride_h, alpha, qscale, page_size, H, Hkv, splits,
+                                  max_tokens, workspace);
   hipStream_t s = (hipStream_t)stream;
   const int G = H / Hkv;
   const bool head_path = B * Hkv >= kHeadPathMinHeads;
@@ -749,4 +881,101 @@ extern "C" int ekv_paged_entmax_decode(
       });
     });
   });
+}
+
+extern "C" int ekv_topk_paged_entmax_decode(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kmin, const void* kmax,
+    int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, void* scores, int num_pages,
+    int seq_len, int q_pos, int k_select, int last_page, const void* k, const void* v,
+    int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+    int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h,
+    const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
+    const int32_t* q_seqlens, const float* alibi_slopes, float* tau, int niter, void* out,
+    int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale, int page_size, int B,
+    int H, int Hkv, int D, int splits, int max_tokens, void* workspace, int64_t workspace_bytes,
+    int dtype, void* stream) {
+  EKV_REQUIRE(q && kmin && kmax && scores && k && v && page_indices && cache_seqlens && tau &&
+                  out && workspace,
+              "ekv_topk_paged_entmax_decode: null pointer");
+  EKV_REQUIRE(B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0, "ekv_topk_paged_entmax_decode: bad heads");
+  EKV_REQUIRE(num_pages > 0 && k_select > 0 && k_select <= num_pages && page_size > 0,
+              "ekv_topk_paged_entmax_decode: bad page selection (k %d of %d pages)", k_select,
+              num_pages);
+  EKV_REQUIRE(niter >= 0 && alpha > 1.0f && splits > 0 && max_tokens > 0,
+              "ekv_topk_paged_entmax_decode: bad decode parameters");
+  EKV_REQUIRE(workspace_bytes >= ekv_decode_workspace_bytes(B, H, Hkv, D, splits, max_tokens),
+              "ekv_topk_paged_entmax_decode: workspace too small");
+  const int n_slots = k_select + (last_page >= 0 ? 1 : 0);
+  const int G = H / Hkv;
+  auto two_launches = [&]() {
+    int rc = ekv_page_criticality(q, q_stride_b, q_stride_h, kmin, kmax, s_stride_b, s_stride_h,
+                                  s_stride_page, alibi_slopes, scores, B, H, Hkv, D, num_pages,
+                                  page_size, seq_len, q_pos, k_select, last_page, page_indices,
+                                  pi_stride_b, pi_stride_h, dtype, stream);
+    if (rc) return rc;
+    return ekv_paged_entmax_decode(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h,
+                                   kv_stride_row, kv_rows, page_indices, pi_stride_b, pi_stride_h,
+                                   n_slots, cache_seqlens, cs_stride_b, cs_stride_h, q_seqlens,
+                                   alibi_slopes, nullptr, tau, 0, niter, out, out_stride_b,
+                                   out_stride_h, alpha, qscale, page_size, B, H, Hkv, D, splits,
+                                   max_tokens, workspace, workspace_bytes, dtype, stream);
+  };
+  // one launch when every head fills a workgroup and its keys, page table and
+  // scores stay in LDS; otherwise criticality+top-k, then the decode
+  if (B * Hkv < kHeadPathMinHeads || num_pages > topk::kMaxStagedKeys || n_slots > kTablePages)
+    return two_launches();
+  const int tokens = max_tokens < n_slots * page_size ? max_tokens : n_slots * page_size;
+  DecodeArgs a = make_decode_args(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h,
+                                  kv_stride_row, kv_rows, page_indices, pi_stride_b, pi_stride_h,
+                                  n_slots, cache_seqlens, cs_stride_b, cs_stride_h, q_seqlens,
+                                  alibi_slopes, nullptr, tau, 0, niter, out, out_stride_b,
+                                  out_stride_h, alpha, qscale, page_size, H, Hkv, splits,
+                                  max_tokens, workspace);
+  a.stage_cap = tokens;
+  a.scores_ready = 0;
+  SelectArgs t;
+  t.kmin = kmin;
+  t.kmax = kmax;
+  t.ssb = s_stride_b;
+  t.ssh = s_stride_h;
+  t.ssp = s_stride_page;
+  t.scores = scores;
+  t.num_pages = num_pages;
+  t.seq_len = seq_len;
+  t.q_pos = q_pos;
+  t.k = k_select;
+  t.last_page = last_page;
+  t.key_cap = num_pages;
+  hipStream_t s = (hipStream_t)stream;
+  int handled = 0;
+  const int rc = dispatch_dtype(dtype, [&](auto tv) {
+    using T = decltype(tv);
+    return dispatch_lpr<T>(D, [&](auto lpr) {
+      constexpr int LPR = decltype(lpr)::value;
+      return dispatch_group(G, [&](auto gv) {
+        constexpr int GG = decltype(gv)::value;
+        constexpr int UC = GG >= 8 ? 1 : (GG == 1 ? 4 : 8 / GG);
+        constexpr int UD = GG >= 4 ? 2 : 8 / GG;
+        auto kern = topk_decode_kernel<T, LPR, GG, UC, UD>;
+        hipFuncAttributes attr;
+        hipError_t e = hipFuncGetAttributes(&attr, (const void*)kern);
+        if (e != hipSuccess)
+          return set_error(EKV_ERR_HIP, "topk_decode_kernel attributes: %s", hipGetErrorString(e));
+        const int64_t keys = (int64_t)num_pages * 4;
+        const int64_t stage = (int64_t)tokens * GG * 4;
+        const int64_t lds = keys > stage ? keys : stage;
+        if ((int64_t)attr.sharedSizeBytes + lds > kLdsPerWorkgroup) return 0;  // too big: fall back
+        e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds);
+        if (e != hipSuccess)
+          return set_error(EKV_ERR_HIP, "topk_decode_kernel LDS %lld: %s", (long long)lds,
+                           hipGetErrorString(e));
+        hipLaunchKernelGGL(kern, dim3(B * Hkv), dim3(kHeadThreads), (size_t)lds, s, a, t);
+        handled = 1;
+        return check_launch("topk_decode_kernel");
+      });
+    });
+  });
+  if (rc || handled) return rc;
+  return two_launches();
 }

@@ -5,11 +5,8 @@
 
 #include "ekv_common.h"
 
-#ifdef EKV_PHASE_TIMERS
-extern __device__ unsigned long long ekv_crit_timers[4096 * 8];
-#define EKV_CSTAMP(i) \
-  if (threadIdx.x == 0 && blockIdx.x < 4096) ekv_crit_timers[blockIdx.x * 8 + (i)] = wall_clock64()
-#else
+// Phase timestamps (experiment builds define EKV_CSTAMP before including).
+#ifndef EKV_CSTAMP
 #define EKV_CSTAMP(i)
 #endif
 
@@ -52,55 +49,34 @@ template <> struct ScoreKey<float> {
   }
 };
 
-// Per-wave counts of two 1-bit flags, combined into block-exclusive prefixes
-// with one barrier.  `cnt` needs 2 * (NT / 64) ints.
-template <int NT>
-__device__ __forceinline__ void block_flag_prefix(bool f0, bool f1, int* cnt, int& pre0, int& pre1,
-                                                  int& tot0, int& tot1) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const uint64_t m0 = __ballot(f0), m1 = __ballot(f1);
-  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  if (lane == 0) {
-    cnt[2 * wid] = __popcll(m0);
-    cnt[2 * wid + 1] = __popcll(m1);
-  }
-  __syncthreads();
-  int b0 = 0, b1 = 0, t0 = 0, t1 = 0;
-#pragma unroll
-  for (int w = 0; w < NT / 64; ++w) {
-    const int c0 = cnt[2 * w], c1 = cnt[2 * w + 1];
-    if (w < wid) {
-      b0 += c0;
-      b1 += c1;
-    }
-    t0 += c0;
-    t1 += c1;
-  }
-  __syncthreads();
-  pre0 = b0 + __popcll(m0 & below);
-  pre1 = b1 + __popcll(m1 & below);
-  tot0 = t0;
-  tot1 = t1;
-}
-
 // Block-wide top-k over `num_pages` group keys; writes ascending indices to
-// out[0..k) and `last_page` to out[k] when last_page >= 0.  blockDim == NT.
-// The keys come from `lds_keys` when `prestaged`, are staged there first when
-// they fit (`lds_cap` keys), and are otherwise recomputed from the scores on
-// every pass, 8 loads in flight per thread (the scores must be visible to
-// this workgroup: written by a previous launch or by this workgroup).  Radix select: 8 bits per pass
-// from the top, then one pack pass.
+// out[0..k) (and lds_out[0..k) when non-null) and `last_page` to out[k] when
+// last_page >= 0.  blockDim == NT.  The keys come from `lds_keys` when
+// `prestaged`, are staged there first when they fit (`lds_cap` keys), and are
+// otherwise recomputed from the scores on every pass (the scores must be
+// visible to this workgroup: written by a previous launch or by this
+// workgroup).
+//
+// Radix select, 8 bits per pass from the top: one histogram per pass (LDS
+// atomics), then every wave scans the 256 bins itself (DPP prefix sum +
+// ballot) to find the bin of the k-th largest key, so a pass costs one
+// barrier.  The pack gives each wave a contiguous range of pages; ranks come
+// from ballots and the per-wave counts (one barrier).  Keys above the
+// threshold are all taken; of the keys equal to it, the first kk in page
+// order.
 template <typename T, int G, int NT = kThreads>
-__device__ void topk_select_block(const T* __restrict__ s0, int64_t head_stride, int num_pages,
-                                  int k, int last_page, int32_t* __restrict__ out,
-                                  uint32_t* lds_keys, int lds_cap, bool prestaged = false) {
-  __shared__ unsigned hist[256];
-  __shared__ int scan_scratch[NT / 64 + 1];
-  __shared__ int flag_cnt[2 * (NT / 64)];
-  __shared__ int sel_bin, sel_kk;
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int64_t head_stride,
+                                                  int num_pages, int k, int last_page,
+                                                  int32_t* __restrict__ out, uint32_t* lds_keys,
+                                                  int lds_cap, bool prestaged = false,
+                                                  int* lds_out = nullptr) {
+  constexpr int W = NT / 64;
+  constexpr int kPasses = ScoreKey<T>::kBits / 8;
   constexpr int kBatch = 8;
-  constexpr int kThreads = NT;
+  __shared__ unsigned hist[kPasses][256];
+  __shared__ int wave_cnt[2 * W];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
   k = min(k, num_pages);
   const bool staged = prestaged || num_pages <= lds_cap;
   // group key of page p: the maximum over the group's query heads
@@ -110,38 +86,24 @@ __device__ void topk_select_block(const T* __restrict__ s0, int64_t head_stride,
     for (int g = 1; g < G; ++g) kk = max(kk, ScoreKey<T>::key(s0[g * head_stride + p]));
     return kk;
   };
+  auto key_of = [&](int p) -> uint32_t { return staged ? lds_keys[p] : gkey(p); };
+  for (int i = tid; i < kPasses * 256; i += NT) (&hist[0][0])[i] = 0u;
   if (staged && !prestaged) {
-    for (int p0 = 0; p0 < num_pages; p0 += kThreads * kBatch) {
+    for (int p0 = 0; p0 < num_pages; p0 += NT * kBatch) {
       uint32_t kv[kBatch];
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
-        const int p = p0 + j * kThreads + tid;
+        const int p = p0 + j * NT + tid;
         kv[j] = p < num_pages ? gkey(p) : 0u;
       }
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
-        const int p = p0 + j * kThreads + tid;
+        const int p = p0 + j * NT + tid;
         if (p < num_pages) lds_keys[p] = kv[j];
       }
     }
-    __syncthreads();
   }
-  // visits every page key (from LDS when staged) with f(p, key)
-  auto for_keys = [&](auto&& f) {
-    for (int p0 = 0; p0 < num_pages; p0 += kThreads * kBatch) {
-      uint32_t kv[kBatch];
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int p = p0 + j * kThreads + tid;
-        kv[j] = p < num_pages ? (staged ? lds_keys[p] : gkey(p)) : 0u;
-      }
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int p = p0 + j * kThreads + tid;
-        if (p < num_pages) f(p, kv[j]);
-      }
-    }
-  };
+  __syncthreads();
 
   EKV_CSTAMP(2);
   uint32_t thr = 0;
@@ -150,64 +112,180 @@ __device__ void topk_select_block(const T* __restrict__ s0, int64_t head_stride,
   if (k > 0 && !take_all) {
     uint32_t prefix = 0, pmask = 0;
     kk = k;
-    for (int shift = ScoreKey<T>::kBits - 8; shift >= 0; shift -= 8) {
-      if (tid < 256) hist[tid] = 0;
-      __syncthreads();
-      for_keys([&](int, uint32_t key) {
-        if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
-      });
-      __syncthreads();
-      const int bin = 255 - tid;  // thread t < 256 owns bin 255 - t: scan from the top
-      const int c = tid < 256 ? (int)hist[bin] : 0;
-      int tot;
-      const int above = block_excl_scan(c, scan_scratch, &tot);
-      if (tid < 256 && above < kk && above + c >= kk) {
-        sel_bin = bin;
-        sel_kk = kk - above;
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const int shift = ScoreKey<T>::kBits - 8 * (pass + 1);
+      for (int p0 = 0; p0 < num_pages; p0 += NT * kBatch) {
+        uint32_t kv[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int p = p0 + j * NT + tid;
+          kv[j] = p < num_pages ? key_of(p) : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int p = p0 + j * NT + tid;
+          if (p < num_pages && (kv[j] & pmask) == prefix)
+            atomicAdd(&hist[pass][(kv[j] >> shift) & 255u], 1u);
+        }
       }
       __syncthreads();
-      prefix |= ((uint32_t)sel_bin) << shift;
+      // lane l holds bins 255-4l .. 252-4l; the bin where the count from the
+      // top reaches kk is found by every wave independently
+      const int top = 255 - 4 * lane;
+      const int c0 = (int)hist[pass][top], c1 = (int)hist[pass][top - 1];
+      const int c2 = (int)hist[pass][top - 2], c3 = (int)hist[pass][top - 3];
+      const int sum = c0 + c1 + c2 + c3;
+      const int incl = wave_incl_scan(sum);
+      const int excl = incl - sum;
+      const uint64_t hit = __ballot(excl < kk && incl >= kk);
+      const int src = (int)__builtin_ctzll(hit);  // at least kk keys share the prefix
+      int e = excl, bin, rem;
+      if (e + c0 >= kk) {
+        bin = top;
+        rem = kk - e;
+      } else if ((e += c0) + c1 >= kk) {
+        bin = top - 1;
+        rem = kk - e;
+      } else if ((e += c1) + c2 >= kk) {
+        bin = top - 2;
+        rem = kk - e;
+      } else {
+        e += c2;
+        bin = top - 3;
+        rem = kk - e;
+      }
+      bin = __builtin_amdgcn_readlane(bin, src);
+      rem = __builtin_amdgcn_readlane(rem, src);
+      prefix |= ((uint32_t)bin) << shift;
       pmask |= 255u << shift;
-      kk = sel_kk;
-      __syncthreads();
+      kk = rem;
     }
     thr = prefix;
   }
   EKV_CSTAMP(3);
   if (k > 0) {
-    // every key > thr is taken, and the first kk keys == thr in page order
-    int gt_base = 0, eq_base = 0;
-    for (int c0 = 0; c0 < num_pages; c0 += kThreads) {
-      const int p = c0 + tid;
-      bool gt = false, eq = false;
-      if (p < num_pages) {
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const int per = (num_pages + W - 1) / W;
+    const int pw0 = min(num_pages, wid * per), pw1 = min(num_pages, pw0 + per);
+    auto flags = [&](int p, bool& gt, bool& eq) {
+      gt = eq = false;
+      if (p < pw1) {
         if (take_all) {
           gt = true;
         } else {
-          const uint32_t key = staged ? lds_keys[p] : gkey(p);
+          const uint32_t key = key_of(p);
           gt = key > thr;
           eq = key == thr;
         }
       }
-      int gt_pre, eq_pre, gt_tot, eq_tot;
-      block_flag_prefix<NT>(gt, eq, flag_cnt, gt_pre, eq_pre, gt_tot, eq_tot);
-      const int eq_rank = eq_base + eq_pre;
-      if (gt || (eq && eq_rank < kk)) out[gt_base + gt_pre + min(eq_rank, kk)] = p;
-      gt_base += gt_tot;
-      eq_base += eq_tot;
+    };
+    int gt_n = 0, eq_n = 0;
+    for (int r0 = pw0; r0 < pw1; r0 += 64) {
+      bool gt, eq;
+      flags(r0 + lane, gt, eq);
+      gt_n += __popcll(__ballot(gt));
+      eq_n += __popcll(__ballot(eq));
+    }
+    if (lane == 0) {
+      wave_cnt[2 * wid] = gt_n;
+      wave_cnt[2 * wid + 1] = eq_n;
+    }
+    __syncthreads();
+    int gt_base = 0, eq_base = 0;
+    for (int w = 0; w < wid; ++w) {
+      gt_base += wave_cnt[2 * w];
+      eq_base += wave_cnt[2 * w + 1];
+    }
+    for (int r0 = pw0; r0 < pw1; r0 += 64) {
+      const int p = r0 + lane;
+      bool gt, eq;
+      flags(p, gt, eq);
+      const uint64_t mg = __ballot(gt), me = __ballot(eq);
+      const int gt_rank = gt_base + __popcll(mg & below);
+      const int eq_rank = eq_base + __popcll(me & below);
+      if (gt || (eq && eq_rank < kk)) {
+        const int slot = gt_rank + min(eq_rank, kk);
+        out[slot] = p;
+        if (lds_out) lds_out[slot] = p;
+      }
+      gt_base += __popcll(mg);
+      eq_base += __popcll(me);
     }
   }
-  if (tid == 0 && last_page >= 0) out[k] = last_page;
+  if (tid == 0 && last_page >= 0) {
+    out[k] = last_page;
+    if (lds_out) lds_out[k] = last_page;
+  }
   EKV_CSTAMP(4);
 }
 
-// One workgroup of kHeadThreads per (b, kv head): scores every page of the
-// head (16-byte loads, kHeadUnroll pages per row segment in flight), keeps
-// the group-max keys in LDS and, when k_sel >= 0, selects the top-k pages in
-// the same workgroup.  No cross-workgroup communication.
-constexpr int kHeadThreads = 512;
-constexpr int kHeadUnroll = 8;
+// Criticality scan of one (b, kv head) by a workgroup of NT threads: scores
+// of the G query heads for pages [0, num_pages) written to `scores`
+// ([B, H, num_pages], query dtype) and, when `lds_keys` is non-null, the
+// group-max order key of every page kept there.  A row segment of LPR lanes
+// owns one page and loads its min and max rows with 16-byte loads, U pages
+// per segment in flight.  Returns the head's score base pointer.
+template <typename T, int LPR, int G, int NT, int U>
+__device__ __forceinline__ T* criticality_scan_head(
+    const T* __restrict__ q, int64_t qsb, int64_t qsh, const T* __restrict__ kmin,
+    const T* __restrict__ kmax, int64_t ssb, int64_t ssh, int64_t ssp,
+    const float* __restrict__ slopes, T* __restrict__ scores, int H, int num_pages,
+    int page_size, int seq_len, int q_pos, int b, int kvh, uint32_t* lds_keys) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int SEGS = NT / LPR;
+  constexpr int ROUND = SEGS * U;
+  const int seg = threadIdx.x / LPR;
+  const int sl = threadIdx.x % LPR;
+  const int col = sl * VEC;
+  const int h0 = kvh * G;
+  const bool keep_keys = lds_keys != nullptr;
 
+  // q in its storage format plus a per-element "q >= 0" mask: the bound of
+  // element d is kmax where q_d >= 0 and kmin elsewhere (kernels/page_criticality.py:88-95)
+  uint4 qraw[G], qmask[G];
+  float slope[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    qraw[g] = ld16(q + b * qsb + (h0 + g) * qsh + col);
+    qmask[g] = Dot16<T>::nonneg_mask(qraw[g]);
+    slope[g] = slopes ? slopes[h0 + g] : 0.f;
+  }
+  const T* kmn = kmin + b * ssb + kvh * ssh;
+  const T* kmx = kmax + b * ssb + kvh * ssh;
+  T* sbase = scores + ((int64_t)b * H + h0) * num_pages;
+
+  for (int p0 = 0; p0 < num_pages; p0 += ROUND) {
+    uint4 lo[U], hi[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int p = p0 + u * SEGS + seg;
+      if (p < num_pages) {
+        lo[u] = ld16(kmn + (int64_t)p * ssp + col);
+        hi[u] = ld16(kmx + (int64_t)p * ssp + col);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int p = p0 + u * SEGS + seg;
+      uint32_t key = 0;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float acc = Dot16<T>::dot(qraw[g], bit_select(lo[u], hi[u], qmask[g]), 0.f);
+        acc = seg_sum<LPR>(acc);
+        if (slopes) {
+          const int last_pos = min((p + 1) * page_size - 1, seq_len - 1);
+          acc = add_rn(acc, mul_rn(slope[g], (float)(last_pos - q_pos)));
+        }
+        const T sv = from_f<T>(acc);
+        key = max(key, ScoreKey<T>::key(sv));
+        if (p < num_pages && sl == 0) sbase[(int64_t)g * num_pages + p] = sv;
+      }
+      if (keep_keys && p < num_pages && sl == 0) lds_keys[p] = key;
+    }
+  }
+  return sbase;
+}
 
 }  // namespace topk
 }  // namespace ekv

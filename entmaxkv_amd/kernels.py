@@ -228,6 +228,75 @@ def paged_entmax_decode(q, k_cache, v_cache, out, cache_seqlens, page_indices, p
     return out
 
 
+def topk_paged_entmax_decode(q, k_min, k_max, scores, k_select: int, last_page: int,
+                             k_cache, v_cache, out, page_indices, cache_seqlens, page_size: int,
+                             alpha: float, niter: int, seq_len: int, q_pos: int,
+                             alibi_slopes=None, q_seqlens=None,
+                             workspace: DecodeWorkspace | None = None, kv_rows: int | None = None,
+                             taus_out: torch.Tensor | None = None):
+    """Criticality + top-k + exact-tau decode of one step (ekv_topk_paged_entmax_decode).
+
+    Scores the pages [0, scores.shape[2]) into ``scores``, writes the top-k page
+    table (last page at slot k) into ``page_indices`` [B, Hkv, k + 1] and the
+    decode output into ``out``; a single launch when the shape allows it.
+    """
+    require_gpu(q, k_min, k_max, scores, k_cache, v_cache, out, page_indices)
+    batch, nheads, q_len, dim = q.shape
+    num_kv_heads = k_cache.shape[1]
+    assert q_len == 1
+    assert nheads % num_kv_heads == 0, "Query heads must be divisible by KV heads"
+    num_pages = scores.shape[2]
+    if not 1 <= k_select <= num_pages:
+        raise ValueError(f"k={k_select} out of range for {num_pages} pages")
+    if k_min.stride() != k_max.stride():
+        raise ValueError("k_min and k_max must share strides")
+    if k_cache.stride() != v_cache.stride():
+        raise ValueError("k_cache and v_cache must share strides")
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype or scores.dtype != q.dtype:
+        raise TypeError("q, scores, k_cache and v_cache must share a dtype")
+    assert scores.is_contiguous() and tuple(scores.shape[:2]) == (batch, nheads)
+    n_slots = k_select + (1 if last_page >= 0 else 0)
+    assert page_indices.dtype == torch.int32 and page_indices.stride(2) == 1
+    assert tuple(page_indices.shape) == (batch, num_kv_heads, n_slots), "page_indices shape"
+    cache_seqlens = _cache_seqlens_2d(cache_seqlens, batch, num_kv_heads)
+    max_tokens = n_slots * page_size
+    if workspace is None:
+        workspace = DecodeWorkspace(batch, nheads, num_kv_heads, dim, choose_splits(max_tokens),
+                                    max_tokens, q.device)
+    elif workspace.spec[:4] != (batch, nheads, num_kv_heads, dim) or workspace.max_tokens < max_tokens:
+        raise ValueError(f"invalid paged workspace {workspace.spec} for shape "
+                         f"{(batch, nheads, num_kv_heads, dim, max_tokens)}")
+    tau = workspace.taus if taus_out is None else taus_out
+    assert tuple(tau.shape) == (batch, nheads) and tau.dtype == torch.float32 and tau.is_contiguous()
+    q3 = _row_major_d(q[:, :, 0], "q")
+    o3 = out[:, :, 0]
+    direct = o3.stride(-1) == 1 and o3.data_ptr() % 16 == 0
+    o_target = o3 if direct else torch.empty(batch, nheads, dim, device=q.device, dtype=q.dtype)
+    slopes = None
+    if alibi_slopes is not None:
+        slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
+    qsl = None
+    if q_seqlens is not None:
+        qsl = q_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
+    if kv_rows is None:
+        kv_rows = k_cache.shape[2]
+    call("ekv_topk_paged_entmax_decode",
+         q3.data_ptr(), q3.stride(0), q3.stride(1), k_min.data_ptr(), k_max.data_ptr(),
+         k_min.stride(0), k_min.stride(1), k_min.stride(2), scores.data_ptr(), num_pages,
+         seq_len, q_pos, k_select, last_page, k_cache.data_ptr(), v_cache.data_ptr(),
+         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), kv_rows,
+         page_indices.data_ptr(), page_indices.stride(0), page_indices.stride(1),
+         cache_seqlens.data_ptr(), cache_seqlens.stride(0), cache_seqlens.stride(1),
+         ptr(qsl), ptr(slopes), tau.data_ptr(), niter, o_target.data_ptr(), o_target.stride(0),
+         o_target.stride(1), float(alpha), qscale_for(alpha, dim, q.dtype), page_size, batch,
+         nheads, num_kv_heads, dim, workspace.splits, workspace.max_tokens,
+         workspace.buf.data_ptr(), workspace.buf.numel(), dtype_code(q.dtype),
+         stream_ptr(q.device))
+    if not direct:
+        o3.copy_(o_target)
+    return out
+
+
 def sparse_attention_decode_paged(q, k_cache, v_cache, out, cache_seqlens, page_indices,
                                   page_size, alibi_slopes=None, is_causal=True, alpha=1.5,
                                   niter=10, max_splits=32, bins=16, q_seqlens=None,

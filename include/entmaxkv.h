@@ -90,6 +90,27 @@ int ekv_paged_entmax_decode(const void* q, int64_t q_stride_b, int64_t q_stride_
                             int H, int Hkv, int D, int splits, int max_tokens, void* workspace,
                             int64_t workspace_bytes, int dtype, void* stream);
 
+/* One top-k decode step: criticality scores of pages [0, num_pages), the
+ * top-k page table (+ last_page at slot k) written to page_indices, then the
+ * exact-tau decode (tau_mode 0 of ekv_paged_entmax_decode, `niter` Halley
+ * steps) over the selected pages, tau to tau [B, H].  Arguments mean what they
+ * mean in ekv_page_criticality and ekv_paged_entmax_decode; ALiBi slopes serve
+ * both.  When every (b, kv head) fits one workgroup with its keys, page table
+ * and scores in LDS this is a single launch, otherwise the two calls above.
+ * Replaces the selection + decode sequence of sparse_attention_decode_paged,
+ * attention_topk.py:45-98. */
+int ekv_topk_paged_entmax_decode(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kmin, const void* kmax,
+    int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, void* scores, int num_pages,
+    int seq_len, int q_pos, int k_select, int last_page, const void* k, const void* v,
+    int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+    int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h,
+    const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
+    const int32_t* q_seqlens, const float* alibi_slopes, float* tau, int niter, void* out,
+    int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale, int page_size, int B,
+    int H, int Hkv, int D, int splits, int max_tokens, void* workspace, int64_t workspace_bytes,
+    int dtype, void* stream);
+
 /* Workspace for ekv_gaussian_page_stats. */
 int64_t ekv_gaussian_workspace_bytes(int B, int H, int Hkv, int D, int pages, int dtype);
 

@@ -301,17 +301,27 @@ def test_decode_edge_cases():
 # public top-k API end to end
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("dtype,G", [("fp16", 1), ("bf16", 4), ("fp32", 1)])
-def test_topk_api_end_to_end(dtype, G):
+# "split": few heads (criticality + top-k launch, then the decode launches);
+# "head": one fused launch per step (criticality, top-k and decode per workgroup)
+TOPK_API_CASES = [("fp16", 1, "split", False), ("bf16", 4, "split", False),
+                  ("fp32", 1, "split", False), ("fp16", 1, "head", False),
+                  ("bf16", 4, "head", False), ("fp32", 2, "head", False),
+                  ("fp16", 1, "head", True), ("bf16", 8, "head", True)]
+
+
+@pytest.mark.parametrize("dtype,G,path,alibi", TOPK_API_CASES)
+def test_topk_api_end_to_end(dtype, G, path, alibi):
     from entmaxkv_amd import sparse_attention_decode_paged
-    _case(test="topk_api", dtype=dtype, G=G)
+    _case(test="topk_api", dtype=dtype, G=G, path=path, alibi=alibi)
     rng = np.random.default_rng(21)
-    B, Hkv, S0, D, ps = 2, 2, 16 * 128, 128, 16
+    B, Hkv = DECODE_SHAPES[path]
+    S0, D, ps = 16 * 128, 128, 16
     H = Hkv * G
     cache, k, v = _build_cache(rng, B, Hkv, S0, D, dtype)
     q = randn(rng, (B, H, 1, D), dtype)
     kn = randn(rng, (B, Hkv, 1, D), dtype)
     vn = randn(rng, (B, Hkv, 1, D), dtype)
+    slopes = np.exp2(-8.0 * np.arange(1, H + 1) / H).astype(np.float32) if alibi else None
     budget = 512
     S = S0 + 1
     P = (S + ps - 1) // ps
@@ -321,23 +331,29 @@ def test_topk_api_end_to_end(dtype, G):
     sparse_attention_decode_paged(
         to_dev(q, dtype), cache, to_dev(kn, dtype), to_dev(vn, dtype), out, budget,
         torch.full((B,), n_sel * ps + lps, dtype=torch.int32, device="cuda"),
-        torch.full((B,), S, dtype=torch.int32, device="cuda"), alpha=1.5, niter=10,
-        append_cache=True)
+        torch.full((B,), S, dtype=torch.int32, device="cuda"),
+        alibi_slopes=None if slopes is None else torch.tensor(slopes, device="cuda"),
+        alpha=1.5, niter=10, append_cache=True)
     torch.cuda.synchronize()
     Kf = np.concatenate([k, kn], axis=2)
     Vf = np.concatenate([v, vn], axis=2)
     st = O.page_stats(Kf, ps, dtype)
     scores = to_np(cache.last_page_scores)
-    ref_scores = O.page_criticality(q[:, :, 0], st[0], st[1], dtype, num_pages=P - 1)
-    if dtype == "fp32":
-        np.testing.assert_allclose(scores, ref_scores, rtol=2e-6, atol=1e-4)
-    else:
-        assert ulp_diff_16(scores, ref_scores, dtype).max() <= 1.0
+    ref_scores = O.page_criticality(q[:, :, 0], st[0], st[1], dtype, num_pages=P - 1,
+                                    alibi_slopes=slopes, page_size=ps, seq_len=S, q_pos=S - 1)
+    # fp32 accumulation order differs from the float64 oracle: bound on the
+    # magnitudes summed (score terms and ALiBi bonus), then one rounding
+    terms = np.abs(O.page_criticality(q[:, :, 0], st[0], st[1], "fp32", num_pages=P - 1))
+    if slopes is not None:
+        terms = terms + np.abs(O.alibi_page_bonus(slopes, P - 1, ps, S, S - 1))[None]
+    ulp = {"fp16": 2.0 ** -10, "bf16": 2.0 ** -7, "fp32": 2.0 ** -23}[dtype]
+    assert (np.abs(scores - ref_scores) <= 2.0 ** -20 * terms + ulp * np.abs(ref_scores)).all()
+    # page table bit-exact given the kernel's scores
     sel = O.topk_pages(O.topk_gqa_group_scores(scores, Hkv), n_sel)
     pidx = np.concatenate([sel, np.full((B, Hkv, 1), P - 1)], axis=2)
     np.testing.assert_array_equal(to_np(cache._page_indices_buf).astype(np.int64), pidx)
     ref, _ = O.paged_entmax_decode(q[:, :, 0], Kf, Vf, pidx, np.full((B, Hkv), n_sel * ps + lps),
-                                   ps, 1.5, 10, dtype, q_seqlens=np.full(B, S))
+                                   ps, 1.5, 10, dtype, alibi_slopes=slopes, q_seqlens=np.full(B, S))
     assert_out_close(to_np(out)[:, :, 0], ref, dtype)
 
 
