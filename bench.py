@@ -5,7 +5,8 @@ appended token, page size 16, fp16, alpha=1.5.  One step = one call of
 ``sparse_attention_decode_paged`` (token budget 1024, niter 2, the cache
 already appended, as in the reference's tests/run_benchmarks.py), with every
 input resident in HBM.  The Gaussian-aware step (tau_mode "corrected") on the
-same shape is reported alongside.
+same shape is reported alongside, on keys drawn as in BASELINE config 3
+(per-head offsets, 2% outlier pages aligned with q; --gauss-keys iid for N(0, 1)).
 
 value = effective bytes per step / step time, where the effective bytes are
 the selected K and V rows, one criticality bound per (b, h, page, d), q and
@@ -47,6 +48,9 @@ def _args():
     p.add_argument("--no-graph", action="store_true", help="time eager launches only")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-gaussian", action="store_true")
+    p.add_argument("--gauss-keys", choices=["c3", "iid"], default="c3",
+                   help="keys of the Gaussian-aware step: c3 = N(mu_h, 1) per head with 2%% "
+                        "outlier pages scaled x3 toward q (BASELINE config 3), iid = N(0, 1)")
     p.add_argument("--only", choices=["topk", "gaussian", "criticality"], default=None,
                    help="run one step kind in a loop (for profilers)")
     p.add_argument("--copy-calib-mib", type=int, default=0,
@@ -79,6 +83,41 @@ def _graphed(fn, stream):
         fn()
     torch.cuda.synchronize()
     return g.replay
+
+
+def _gaussian_cache(B, H, Hkv, L, D, ps, dt, dev, q, kind):
+    """Cache for the Gaussian-aware step (seeded, built on the device).
+
+    c3: keys ~ N(mu_h, 1) with mu_h ~ N(0, 0.5) per (b, kv head); 2% of the
+    pages of each (b, kv head), chosen at random, become 3 * (k + 4 q_hat),
+    q_hat the unit query of the group's first head; values ~ N(0, 1).
+    """
+    import torch
+
+    from entmaxkv_amd import PagedKVCache
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    k = torch.randn(B, Hkv, L, D, device=dev, dtype=torch.float32, generator=g)
+    if kind == "c3":
+        k += torch.randn(B, Hkv, 1, 1, device=dev, generator=g) * math.sqrt(0.5)
+        P = L // ps
+        n_out = max(1, int(0.02 * P))
+        G = H // Hkv
+        qh = q[:, ::G, 0].float()
+        qh = qh / qh.norm(dim=-1, keepdim=True)  # [B, Hkv, D]
+        pages = torch.argsort(torch.rand(B, Hkv, P, device=dev, generator=g), dim=-1)[..., :n_out]
+        kp = k[:, :, : P * ps].view(B, Hkv, P, ps, D)
+        idx = pages[..., None, None].expand(B, Hkv, n_out, ps, D)
+        sel = torch.gather(kp, 2, idx)
+        sel = 3.0 * (sel + 4.0 * qh[:, :, None, None, :])
+        kp.scatter_(2, idx, sel)
+    k = k.to(dt)
+    v = torch.randn(B, Hkv, L, D, device=dev, dtype=torch.float32, generator=g).to(dt)
+    cache = PagedKVCache(page_size=ps)
+    cache.initialize(k, v)
+    del k, v
+    return cache
 
 
 def main():
@@ -144,8 +183,10 @@ def main():
             del src, dst
         fn = {"topk": topk_step, "criticality": crit_only}.get(a.only)
         if a.only == "gaussian":
+            gcache = _gaussian_cache(B, H, Hkv, S, D, ps, dt, dev, q, a.gauss_keys)
+
             def fn():
-                sparse_attention_decode_gaussian_aware_entmax(q, cache, k_new, v_new, out,
+                sparse_attention_decode_gaussian_aware_entmax(q, gcache, k_new, v_new, out,
                                                               alpha=a.alpha, tau_mode="corrected")
         ms = _time_loop(fn, a.steps, a.warmup, stream)
         print(json.dumps({"only": a.only, "ms_per_step": ms}), flush=True)
@@ -158,30 +199,39 @@ def main():
         ms_graph = _time_loop(replay, a.steps, a.warmup, stream)
     ms = ms_graph if ms_graph is not None else ms_eager
 
-    # dominant kernel: criticality (+ fused top-k); average launch time over the timed loop
-    ms_crit = _time_loop(crit_only if a.no_graph else _graphed(crit_only, stream), a.steps,
-                         a.warmup, stream)
-    crit_alg = crit_bytes + B * H * (P - 1) * esz  # bounds read + scores written
-    crit_gbs = crit_alg / (ms_crit * 1e-3) / 1e9
+    # Dominant (and only) kernel of the step: topk_decode_kernel (criticality,
+    # top-k, tau and the weighted sum per workgroup).  Its average launch
+    # duration is the step time of the replayed graph, timed with events on
+    # the stream it is launched on.
+    fused = B * Hkv >= 128
+    roof_kernel = "topk_decode_kernel" if fused else "criticality_head_kernel + decode kernels"
+    launch_gbs = step_bytes / (ms * 1e-3) / 1e9
 
     gauss = None
     if not a.no_gaussian:
+        gcache = _gaussian_cache(B, H, Hkv, S, D, ps, dt, dev, q, a.gauss_keys)
+
         def gauss_step():
-            sparse_attention_decode_gaussian_aware_entmax(q, cache, k_new, v_new, out,
+            sparse_attention_decode_gaussian_aware_entmax(q, gcache, k_new, v_new, out,
                                                           alpha=a.alpha, tau_mode="corrected")
         gms_eager = _time_loop(gauss_step, a.steps, a.warmup, stream)
         gms_graph = None
         if not a.no_graph:
             greplay = _graphed(gauss_step, stream)
             gms_graph = _time_loop(greplay, a.steps, a.warmup, stream)
-        sel = cache.last_num_selected_per_head.double()
-        sel_tok = float(((sel - 1).clamp(min=0) * ps + lps).sum().item())
-        g_bytes = B * Hkv * (P - 1) * D * esz * 2 + sel_tok * D * esz * 2 + io_bytes
+        gP = gcache.num_pages
+        glps = S - (gP - 1) * ps
+        sel = gcache.last_num_selected_per_head.double()
+        sel_tok = float(((sel - 1).clamp(min=0) * ps + glps).sum().item())
+        # moments read once per kv head + the selected K rows (V only on the support,
+        # counted in full as an upper bound of the algorithmic bytes)
+        g_bytes = B * Hkv * (gP - 1) * D * esz * 2 + sel_tok * D * esz * 2 + io_bytes
         gms = gms_graph if gms_graph is not None else gms_eager
-        gauss = {"us_per_step": gms * 1e3, "us_eager": gms_eager * 1e3,
-                 "effective_GBs": g_bytes / (gms * 1e-3) / 1e9,
-                 "pct_hbm_peak": 100.0 * g_bytes / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                 "mean_selected_pages": float(sel.mean().item()),
+        gauss = {"keys": a.gauss_keys, "us_per_step": round(gms * 1e3, 2),
+                 "us_eager": round(gms_eager * 1e3, 2),
+                 "effective_GBs": round(g_bytes / (gms * 1e-3) / 1e9, 1),
+                 "pct_hbm_peak": round(100.0 * g_bytes / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                 "mean_selected_pages": round(float(sel.mean().item()), 2),
                  "bytes_per_step": g_bytes}
 
     cpu = None
@@ -210,23 +260,23 @@ def main():
                    "token_budget": a.budget, "selected_tokens_per_head": n_tok,
                    "alpha": a.alpha, "niter": a.niter, "timing": "hipGraph replay" if ms_graph else "eager",
                    "bytes_per_step": step_bytes},
-        "roofline": {"bound": "hbm", "kernel": "criticality_head_kernel (fused top-k)",
-                     "achieved": round(crit_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(crit_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "avg_launch_us": round(ms_crit * 1e3, 2), "bytes_per_launch": crit_alg},
+        "roofline": {"bound": "hbm", "kernel": roof_kernel,
+                     "achieved": round(launch_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(launch_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_launch_us": round(ms * 1e3, 2), "bytes_per_launch": step_bytes},
         "gaussian": gauss,
         "cpu_baseline": cpu,
     }
     headline = (B, H, Hkv, D, L, a.budget, a.dtype) == (8, 32, 32, 128, 32768, 1024, "fp16")
-    traffic = _measured_traffic("criticality_head_kernel") if headline else None
+    traffic = _measured_traffic("topk_decode_kernel") if headline and fused else None
     if traffic:
         line["roofline"]["traffic"] = traffic
-        line["roofline"]["frac_traffic"] = round(traffic / (ms_crit * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        line["roofline"]["frac_traffic"] = round(traffic / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
     print(json.dumps(line), flush=True)
     return 0
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "criticality_head_kernel_pmc_b8h32l32k.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "topk_decode_kernel_pmc_b8h32l32k.md")
 
 
 def _measured_traffic(kernel_tag):

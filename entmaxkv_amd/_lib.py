@@ -44,6 +44,12 @@ SIGNATURES = {
     "ekv_gaussian_workspace_bytes": (I64, [I, I, I, I, I, I]),
     "ekv_gaussian_page_stats": (I, [P, I64, I64, P, P, I64, I64, I64, I, P, I, I, P, P, P, P, P,
                                     P, P, F, I, I, F, I, I, I, I, P, I64, I, P]),
+    "ekv_gaussian_moments": (I, [P, I64, I64, P, P, I64, I64, I64, I, P, I, I, I, P, P, I, I, I,
+                                 I, P, I64, I, P]),
+    "ekv_gaussian_paged_entmax_decode": (I, [P, I64, P, P, I, I, P, P, P, P, P, I, I, I, F, I, F,
+                                             F, F, F, F, P, I64, I64, P, P, P, I, P, F, F, P, P,
+                                             I64, I64, P, P, I64, I64, I64, I64, P, P, P, I, I, P,
+                                             I64, I64, F, F, I, I, I, I, I, I, P, I64, I, P]),
     "ekv_tau_single_gaussian": (I, [P, P, P, I, I, F, I, F, P]),
     "ekv_tau_page_mixture": (I, [P, P, P, I, I, F, F, I, F, P]),
     "ekv_select_gaussian_pack": (I, [P, P, P, P, I, I, I, I, I, F, I, F, F, F, F, F, P, I64, I64,
@@ -52,7 +58,7 @@ SIGNATURES = {
     "ekv_cache_seqlens_from_counts": (I, [P, P, I, I, I, P]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib = None

@@ -9,7 +9,7 @@ from typing import Optional
 import torch
 
 from . import kernels as K
-from .gaussian_utils import compute_gaussian_aware_statistics
+from .gaussian_utils import solve_for_tau_hat_page_gaussian_mixture_auto, stats_dict
 from .kv_cache import PagedKVCache
 
 
@@ -41,8 +41,10 @@ def sparse_attention_decode_gaussian_aware_entmax(
     ``tau_correction_iters`` (default 1, 2 with ALiBi) Halley corrections.
     As in the reference, ``safety_margin_z`` and ``max_quantile`` are superseded
     by the automatic margins and ``scale`` is unused (the kernel uses 1/sqrt(D)).
-    Launches: [append] -> page moments + tau-hat -> [mixture tau-hat] ->
-    select + pack + clamp + lengths -> scores + tau -> weighted sum.
+    Launches: [append] -> page moments -> [page-mixture tau-hat under ALiBi]
+    -> one launch of global moments + tau-hat + select + pack + clamp +
+    decode (separate launches when batch * kv heads is too small to fill the
+    GPU).
     """
     batch, num_heads, _, head_dim = q.shape
 
@@ -64,42 +66,54 @@ def sparse_attention_decode_gaussian_aware_entmax(
     num_pages = kv_cache.num_pages
     pages_for_stats = num_pages - 1 if num_pages > 1 else num_pages
 
-    gaussian_stats = compute_gaussian_aware_statistics(
-        q=q, k_mean=kv_cache.k_mean, k_std=kv_cache.k_std, seq_len=seq_len, page_size=page_size,
-        alpha=alpha, alibi_slopes=alibi_slopes,
-        threshold_excess_margin_fraction=threshold_excess_margin_fraction,
-        tau_clamp_page_max_quantile=tau_clamp_page_max_quantile,
-        buffers=kv_cache.get_gaussian_buffers(q, pages_for_stats))
+    last_page_tokens = seq_len - (num_pages - 1) * page_size if num_pages > 1 else 0
+    seq_len_for_stats = seq_len - last_page_tokens
+    if alpha not in (2, 1.5, 4 / 3):
+        raise ValueError(f"Unsupported alpha for the Gaussian tau solve: {alpha}")
+    buf = kv_cache.get_gaussian_buffers(q, pages_for_stats)
+    K.compute_page_gaussian_moments(q, kv_cache.k_mean, kv_cache.k_std, pages_for_stats, buf,
+                                    alibi_slopes=alibi_slopes, page_size=page_size,
+                                    seq_len=seq_len, n_tokens=seq_len_for_stats)
+    tau_hat_given = alibi_slopes is not None
+    if tau_hat_given:
+        # ALiBi: page-mixture tau-hat over the biased page means (gaussian_utils.py:171-181)
+        tau_mix = solve_for_tau_hat_page_gaussian_mixture_auto(
+            buf.mu_p, buf.sigma_p, alpha=alpha, uniform_page_count=float(page_size))
+        buf.tau_hat.copy_(tau_mix.squeeze(-1))
+    gaussian_stats = stats_dict(buf, seq_len_for_stats, pages_for_stats, num_pages,
+                                threshold_excess_margin_fraction, tau_clamp_page_max_quantile)
 
     last_page_size = (seq_len - (math.ceil(seq_len / page_size) - 1) * page_size
                       if seq_len > page_size else seq_len)
     do_clamp = needs_tau and clamp_tau
-    page_indices, _ = kv_cache.select_gaussian_aware(
-        q, alpha=alpha, safety_margin_z=safety_margin_z, max_quantile=max_quantile,
-        gaussian_stats=gaussian_stats, clamp=do_clamp, last_page_size=last_page_size)
-    cache_seqlens = gaussian_stats["cache_seqlens"]
-
+    sb = kv_cache._get_select_buffers(batch, num_heads, kv_cache._k.shape[1], num_pages,
+                                      q.device)
     workspace = kv_cache.get_paged_decode_workspace(
         batch, num_heads, head_dim, splits, 16, q.dtype, q.device,
-        max_tokens=page_indices.shape[2] * page_size)
-
+        max_tokens=num_pages * page_size)
     if tau_mode == "exact":
-        K.paged_entmax_decode(
-            q, kv_cache._k, kv_cache._v, out, cache_seqlens, page_indices, page_size, alpha,
-            tau_mode=0, iters=niter, tau=None, alibi_slopes=alibi_slopes, q_seqlens=q_seqlens,
-            workspace=workspace, kv_rows=kv_cache.kv_capacity)
+        dec_mode, iters = 0, niter
     else:
+        dec_mode = 1
         if tau_correction_iters is None:
             if tau_mode == "fixed":
                 tau_correction_iters = 0
             else:
                 tau_correction_iters = 1 if alibi_slopes is None else 2
-        tau0 = gaussian_stats["tau_clamped"] if do_clamp else gaussian_stats["tau_hat"]
-        K.paged_entmax_decode(
-            q, kv_cache._k, kv_cache._v, out, cache_seqlens, page_indices, page_size, alpha,
-            tau_mode=1, iters=tau_correction_iters, tau=workspace.taus, tau_in=tau0,
-            alibi_slopes=alibi_slopes, q_seqlens=q_seqlens, workspace=workspace,
-            kv_rows=kv_cache.kv_capacity)
+        iters = tau_correction_iters
+    K.gaussian_paged_entmax_decode(
+        q, kv_cache._k, kv_cache._v, out, buf, pages_for_stats=pages_for_stats,
+        num_pages=num_pages, n_tokens=seq_len_for_stats, page_size=page_size, alpha=alpha,
+        tau_hat_given=tau_hat_given, safety_margin_z=None, max_quantile=None,
+        threshold_excess_margin_fraction=threshold_excess_margin_fraction,
+        page_indices=sb["page_indices"], counts=sb["counts"], tau_floor=sb["tau_floor"],
+        cache_seqlens=sb["cache_seqlens"], last_page_size=last_page_size,
+        tau_clamped=sb["tau_clamped"] if do_clamp else None,
+        clamp_quantile=tau_clamp_page_max_quantile, effective=sb["effective"],
+        tau_out=workspace.taus, tau_mode=dec_mode, iters=iters, workspace=workspace,
+        alibi_slopes=alibi_slopes, q_seqlens=q_seqlens, kv_rows=kv_cache.kv_capacity)
+    kv_cache.record_gaussian_selection(gaussian_stats, sb, do_clamp)
+    if tau_mode != "exact":
         gaussian_stats["tau_final"] = workspace.taus
     kv_cache.last_gaussian_stats = gaussian_stats
     return out

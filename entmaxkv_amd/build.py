@@ -3,6 +3,8 @@
 Usage: python -m entmaxkv_amd.build   (or call build()).
 Each source compiles in parallel to an object under entmaxkv_amd/_build/, then
 one link writes the library next to this file so it travels with the tree.
+decode_inst.hip compiles once per (storage dtype, GQA group) pair, so the
+decode kernels of different pairs build in parallel.
 """
 
 from __future__ import annotations
@@ -26,6 +28,13 @@ CFLAGS = [
 ]
 
 
+# sources compiled once per variant: file -> [(object tag, -D flags)]
+INSTANCES = {
+    "decode_inst.hip": [(f".t{t}.g{g}", [f"-DEKV_INST_DTYPE={t}", f"-DEKV_INST_G={g}"])
+                        for t in (0, 1, 2) for g in (1, 2, 4, 8)],
+}
+
+
 def hipcc() -> str:
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
     cand = os.path.join(rocm, "bin", "hipcc")
@@ -45,9 +54,12 @@ def build(verbose: bool = False) -> str:
     inc = ["-I", os.path.join(HERE, "..", "include")]
     objs, cmds = [], []
     for src in srcs:
-        obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-        objs.append(obj)
-        cmds.append([hipcc(), *CFLAGS, *inc, "-c", src, "-o", obj])
+        base = os.path.basename(src)
+        variants = INSTANCES.get(base, [("", [])])
+        for tag, defs in variants:
+            obj = os.path.join(OBJ, base + tag + ".o")
+            objs.append(obj)
+            cmds.append([hipcc(), *CFLAGS, *defs, *inc, "-c", src, "-o", obj])
     workers = min(len(cmds), max(1, (os.cpu_count() or 2)))
     with cf.ThreadPoolExecutor(workers) as ex:
         for cmd, fut in zip(cmds, [ex.submit(_run, c) for c in cmds]):

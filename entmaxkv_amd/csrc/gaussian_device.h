@@ -1,0 +1,472 @@
+// Device-side building blocks of the Gaussian-aware page selection, shared by
+// the standalone launches (gaussian_select.hip) and the fused select + decode
+// launch (paged_decode.hip).
+//
+//   gaussian_terms / solve_*      tau_solver.py:31-120, 347-412 and
+//                                 kernels/tau_solver_gpu.py:20-125
+//   moments_partial_block         kernels/gaussian_page_stats.py:8-121 and
+//                                 gaussian_utils.py:130-161 (per-page moments
+//                                 and this workgroup's share of the global sums)
+//   finalize_moments              gaussian_utils.py:155-161
+//   select_pack_block             kernels/selection_pack.py:113-198,
+//                                 gaussian_utils.py:163-169 (automatic
+//                                 margins), kernels/tau_clamp.py:8-73,
+//                                 kernels/selection_pack.py:7-20
+//
+// The global moments of a head are reduced from per-workgroup partial sums
+// (Sum mu_p, Sum mu_p^2, Sum sigma_p^2) that the moments launch writes with
+// plain stores; whoever needs mu_g / sigma_g sums a head's partials in a fixed
+// order, so every consumer derives bit-identical values and no workgroup ever
+// waits for another.
+#pragma once
+
+#include "ekv_common.h"
+
+namespace ekv {
+namespace gauss {
+
+// Workgroups per (b, kv head) of the moments launch: about 1024 workgroups in
+// all, at least 64 pages each, at most 64 per head.
+inline int moment_splits(int bkv, int pages) {
+  int s = (1024 + bkv - 1) / bkv;
+  const int by_pages = (pages + 63) / 64;
+  if (s > by_pages) s = by_pages;
+  if (s > 64) s = 64;
+  return s < 1 ? 1 : s;
+}
+
+// Host launcher (gaussian_select.hip) of the global moments and tau-hat from
+// the moments launch's partials (tau_hat may be null); the fused entry point's
+// fallback uses it.
+int launch_finalize(const void* partials, int B, int H, int Hkv, int pages, float* mu_g,
+                    float* sigma_g, float* mean_var, float* var_means, float* tau_hat, float alpha,
+                    int n_tokens, int tau_iters, float tol, hipStream_t stream);
+
+__device__ __forceinline__ float normal_pdf(float x) {
+  return expf(-0.5f * x * x) * 0.3989422804014327f;
+}
+// Phi(x) = 0.5 * erfc(-x / sqrt(2)): equal to 0.5 * (1 + erf(x / sqrt(2))) but
+// without the cancellation of 1 + erf in the lower tail.
+__device__ __forceinline__ float normal_cdf(float x) {
+  return 0.5f * erfcf(-x * 0.7071067811865476f);
+}
+
+// f(tau) = n*E[[(alpha-1)S - tau]_+^(1/(alpha-1))] for S ~ N(mu, sigma^2)
+// (count weight `n`), with first and second derivatives in tau.  The third
+// moment used for alpha = 4/3 is the reference's expression
+// (tau_solver.py:104-107).
+__device__ __forceinline__ void gaussian_terms(float tau, float mu, float sigma, float n,
+                                               float alpha, float& e, float& d1, float& d2) {
+  const float a = alpha - 1.0f;
+  const float sy = fmaxf(a * sigma, 1.0e-10f);
+  const float my = a * mu - tau;
+  const float t = my / sy;
+  const float ph = normal_pdf(t);
+  const float Ph = normal_cdf(t);
+  const float m0 = Ph;
+  const float m1 = my * Ph + sy * ph;
+  const float m2 = (my * my + sy * sy) * Ph + my * sy * ph;
+  if (alpha == 2.0f) {
+    e = n * m1;
+    d1 = -n * m0;
+    d2 = n * ph / sy;
+  } else if (alpha == 1.5f) {
+    e = n * m2;
+    d1 = -2.0f * n * m1;
+    d2 = 2.0f * n * m0;
+  } else {
+    const float m3 = (my * my * my + 3.0f * my * sy * sy) * Ph + (sy * sy * sy + 2.0f * my * my * sy) * ph;
+    e = n * m3;
+    d1 = -3.0f * n * m2;
+    d2 = 6.0f * n * m1;
+  }
+}
+
+// One bracketed Halley step with bisection fallback (tau_solver.py:380-410):
+// updates (t, lo, hi); returns true once a candidate is accepted after a step
+// below 1e-6 * max(1, |t|).
+__device__ __forceinline__ bool halley_bracket_step(float& t, float& lo, float& hi, float mu,
+                                                    float sigma, float n, float alpha, float tol) {
+  float e, f1, f2;
+  gaussian_terms(t, mu, sigma, n, alpha, e, f1, f2);
+  const float f = e - 1.0f;
+  const float mid = 0.5f * (lo + hi);
+  const float den = 2.0f * f1 * f1 - f * f2;
+  const float step = fabsf(den) > 1.0e-18f ? 2.0f * f * f1 / den : f / fminf(f1, -1.0e-12f);
+  float cand = t - step;
+  if (!(cand == cand && fabsf(cand) < 1.0e20f && cand > lo && cand < hi)) cand = mid;
+  float ec, u1, u2;
+  gaussian_terms(cand, mu, sigma, n, alpha, ec, u1, u2);
+  const float fc = ec - 1.0f;
+  if (fc > 0.0f) lo = cand;
+  else hi = cand;
+  if (fabsf(fc) <= tol) {
+    const bool small = fabsf(cand - t) <= 1.0e-6f * fmaxf(1.0f, fabsf(t));
+    t = cand;
+    return small;
+  }
+  t = 0.5f * (lo + hi);
+  return false;
+}
+
+// Single-Gaussian tau-hat solved by one lane: the reference's bracket
+// (alpha-1)mu +- (alpha-1)sigma(sqrt(2 ln(n+1)) + 8) and up to `iterations`
+// bracketed Halley steps, stopping early once a step is accepted.
+__device__ __forceinline__ float solve_single_gaussian(float mu, float sigma, float n, float alpha,
+                                                       float log_n_factor, int iterations,
+                                                       float tol) {
+  sigma = fmaxf(sigma, 1.0e-6f);
+  const float a = alpha - 1.0f;
+  const float radius = a * sigma * (log_n_factor + 8.0f);
+  float lo = a * mu - radius, hi = a * mu + radius;
+  float t = 0.5f * (lo + hi);
+  for (int it = 0; it < iterations; ++it)
+    if (halley_bracket_step(t, lo, hi, mu, sigma, n, alpha, tol)) break;
+  return t;
+}
+
+// The same root solved by a whole wave (every lane returns it): three rounds
+// of a 64-point bracket search (f is decreasing in tau, so the positive lanes
+// form a prefix; the bracket shrinks 65x per round), then bracketed Halley
+// steps from the middle of the final bracket.  Ten function evaluations
+// instead of up to 2 * iterations on one lane.
+__device__ __forceinline__ float solve_single_gaussian_wave(float mu, float sigma, float n,
+                                                            float alpha, float log_n_factor,
+                                                            int iterations, float tol) {
+  sigma = fmaxf(sigma, 1.0e-6f);
+  const float a = alpha - 1.0f;
+  const float radius = a * sigma * (log_n_factor + 8.0f);
+  float lo = a * mu - radius, hi = a * mu + radius;
+  const int lane = threadIdx.x & 63;
+#pragma unroll 1
+  for (int r = 0; r < 3; ++r) {
+    const float w = (hi - lo) * (1.0f / 65.0f);
+    const float x = fmaf(w, (float)(lane + 1), lo);
+    float e, d1, d2;
+    gaussian_terms(x, mu, sigma, n, alpha, e, d1, d2);
+    const uint64_t pos = __ballot(e - 1.0f > 0.0f);
+    // last lane with f > 0 (lanes past it read f <= 0)
+    const int k = pos ? 64 - __builtin_clzll(pos) : 0;
+    const float nlo = k > 0 ? fmaf(w, (float)k, lo) : lo;
+    const float nhi = k < 64 ? fmaf(w, (float)(k + 1), lo) : hi;
+    lo = nlo;
+    hi = fmaxf(nhi, nlo);
+  }
+  float t = 0.5f * (lo + hi);
+  const int steps = iterations < 4 ? iterations : 4;
+  for (int it = 0; it < steps; ++it)
+    if (halley_bracket_step(t, lo, hi, mu, sigma, n, alpha, tol)) break;
+  return t;
+}
+
+// ---------------------------------------------------------------------------
+// per-page moments and per-workgroup partial sums
+// ---------------------------------------------------------------------------
+
+struct MomentsArgs {
+  const void* q;
+  int64_t qsb, qsh;
+  const void* kmean;
+  const void* kstd;
+  int64_t ssb, ssh, ssp;
+  int pages;            // pages_for_stats
+  int pages_per_split;  // pages handled by one workgroup
+  int splits;           // workgroups per (b, kv head)
+  int H, Hkv;
+  float scale;          // 1/sqrt(D) in fp32
+  const float* slopes;  // ALiBi [H] or null
+  int page_size;
+  int q_pos;            // seq_len - 1
+  int stats_len;        // seq_len_for_stats
+  float* mu_p;          // [B, H, pages]
+  float* sigma_p;       // [B, H, pages]
+  float4* partials;     // [B, H, splits] (Sum mu, Sum mu^2, Sum var, 0)
+};
+
+// Moments of pages [split * pages_per_split, ...) of one (b, kv head) for its
+// G query heads:
+//   mu_p = sum_d (q_d/sqrt(D)) mean_pd (+ ALiBi page-mean bias),
+//   sigma_p = sqrt(sum_d (q_d/sqrt(D))^2 std_pd^2),
+// and the workgroup's partial sums (of the unbiased mu_p).  A row segment of
+// LPR lanes owns a page; U pages per segment in flight.  blockDim == NT.
+template <typename T, int LPR, int G, int NT, int U>
+__device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int b, int kvh,
+                                                      int split) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int SEGS = NT / LPR;
+  constexpr int W = NT / 64;
+  __shared__ float4 red[G][W];
+  const int seg = threadIdx.x / LPR;
+  const int sl = threadIdx.x % LPR;
+  const int col = sl * VEC;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int h0 = kvh * G;
+
+  float qs[G][VEC], qq[G][VEC];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    Vec<T> x;
+    x.load((const T*)a.q + b * a.qsb + (h0 + g) * a.qsh + col);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      qs[g][i] = x.v[i] * a.scale;
+      qq[g][i] = qs[g][i] * qs[g][i];
+    }
+  }
+  const T* km = (const T*)a.kmean + b * a.ssb + kvh * a.ssh;
+  const T* ks = (const T*)a.kstd + b * a.ssb + kvh * a.ssh;
+  const int p_begin = split * a.pages_per_split;
+  const int p_end = min(a.pages, p_begin + a.pages_per_split);
+  float s_mu[G], s_mu2[G], s_var[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) s_mu[g] = s_mu2[g] = s_var[g] = 0.f;
+
+  for (int p0 = p_begin; p0 < p_end; p0 += SEGS * U) {
+    VecRaw<T> mv[U], sv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int p = p0 + u * SEGS + seg;
+      if (p < p_end) {
+        mv[u].load(km + (int64_t)p * a.ssp + col);
+        sv[u].load(ks + (int64_t)p * a.ssp + col);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int p = p0 + u * SEGS + seg;
+      const bool ok = p < p_end;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float mu = 0.f, var = 0.f;
+        if (ok) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            const float sd = sv[u].get(i);
+            mu += mv[u].get(i) * qs[g][i];
+            var += (sd * sd) * qq[g][i];
+          }
+        }
+        mu = seg_sum<LPR>(mu);
+        var = seg_sum<LPR>(var);
+        if (ok && sl == 0) {
+          s_mu[g] += mu;
+          s_mu2[g] += mu * mu;
+          s_var[g] += var;
+          const int64_t o = ((int64_t)b * a.H + h0 + g) * a.pages + p;
+          float mub = mu;
+          if (a.slopes) {
+            // gaussian_utils.py:142-153: slope * (min(p*ps + (ps-1)/2, S'-1) - q_pos)
+            const float pos = fminf((float)p * (float)a.page_size + (float)(a.page_size - 1) * 0.5f,
+                                    (float)(a.stats_len - 1));
+            mub = add_rn(mu, mul_rn(a.slopes[h0 + g], sub_rn(pos, (float)a.q_pos)));
+          }
+          a.mu_p[o] = mub;
+          a.sigma_p[o] = sqrtf(var);
+        }
+      }
+    }
+  }
+  // workgroup partials in a fixed order: lanes, then waves
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float x = wave_sum(s_mu[g]), y = wave_sum(s_mu2[g]), z = wave_sum(s_var[g]);
+    if (lane == 0) red[g][wid] = make_float4(x, y, z, 0.f);
+  }
+  __syncthreads();
+  if (threadIdx.x < G) {
+    const int g = threadIdx.x;
+    float4 r = red[g][0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) {
+      r.x += red[g][w].x;
+      r.y += red[g][w].y;
+      r.z += red[g][w].z;
+    }
+    a.partials[((int64_t)b * a.H + h0 + g) * a.splits + split] = r;
+  }
+}
+
+// Sum of one head's partials, in split order.
+__device__ __forceinline__ float4 head_sums(const float4* __restrict__ partials, int64_t head,
+                                            int splits) {
+  const float4* p = partials + head * splits;
+  float4 r = p[0];
+  for (int s = 1; s < splits; ++s) {
+    const float4 y = p[s];
+    r.x += y.x;
+    r.y += y.y;
+    r.z += y.z;
+  }
+  return r;
+}
+
+struct Moments {
+  float mu_g, sigma_g, mean_var, var_means;
+};
+
+// Global moments of a head from its sums over `pages` pages: mean of mu_p,
+// sigma_g = sqrt(mean sigma_p^2 + population variance of mu_p), with the
+// reference's nan/inf clean-up and clamp (gaussian_utils.py:155-161).
+__device__ __forceinline__ Moments finalize_moments(float4 s, int pages) {
+  const float denom = (float)pages;
+  const float mean = s.x / denom;
+  const float mvar = s.z / denom;
+  const float vmeans = fmaxf(s.y / denom - mean * mean, 0.0f);
+  float sg = sqrtf(mvar + vmeans);
+  if (sg != sg) sg = 1e-6f;
+  else if (isinf(sg)) sg = sg > 0 ? 1e6f : 1e-6f;
+  sg = fmaxf(sg, 1e-6f);
+  float mg = mean;
+  if (mg != mg || isinf(mg)) mg = 0.f;
+  return Moments{mg, sg, mvar, vmeans};
+}
+
+// ---------------------------------------------------------------------------
+// threshold selection + pack + clamp + compacted lengths of one (b, kv head)
+// ---------------------------------------------------------------------------
+
+struct SelectArgs {
+  const float* mu_p;
+  const float* sigma_p;
+  int B, H, Hkv;
+  int pages;      // pages_for_stats
+  int num_pages;  // pages incl. the in-progress last page
+  float am1;
+  int auto_margins;
+  float smz;                      // used when !auto_margins
+  float z_page;                   // used when !auto_margins
+  float z_page_low, z_page_high;  // auto: max_quantile 0.99 / 0.995
+  float frac;
+  int32_t* page_indices;
+  int64_t pisb, pish;
+  int32_t* counts;         // [B, Hkv]
+  float* tau_floor;        // [B, H]
+  int32_t* cache_seqlens;  // [B, Hkv] or null
+  int page_size;
+  int last_page_size;
+  float* tau_clamped;      // [B, H] or null
+  float z_clamp;
+  float eps;
+  float* eff;              // [2] = (safety_margin_z, max_quantile) or null
+};
+
+// Selects the pages of one (b, kv head) given each query head's tau-hat
+// (`tau_hat[g]`), sigma_g (`sig_g[g]`) and the batch-wide mean sigma_g
+// (`sbar`, used with automatic margins).  Writes the ascending page table
+// (+ the last page as sentinel) to global memory and, for slots < lds_cap, to
+// `lds_pages`; the count, tau floor, compacted length and (with clamp) the
+// clamped tau, which is also returned in tau_out[g] (tau-hat when not
+// clamping).  Returns the page count.  blockDim == NT; every thread returns
+// the same count.
+template <int G, int NT>
+__device__ __forceinline__ int select_pack_block(const SelectArgs& a, int b, int kvh, float sbar,
+                                                 const float* tau_hat, const float* sig_g,
+                                                 int* lds_pages, int lds_cap, float* tau_out) {
+  __shared__ float scratch[16];
+  __shared__ int scan_scratch[NT / 64 + 1];
+  __shared__ float cm[NT / 64];
+  const int tid = threadIdx.x;
+  const int bkv = b * a.Hkv + kvh;
+  const int h0 = kvh * G;
+
+  float smz = a.smz, z_page = a.z_page;
+  if (a.auto_margins) {
+    const bool low = sbar < 1.5f;
+    smz = (float)((low ? 0.01 : 0.05) * (double)sbar);
+    z_page = low ? a.z_page_low : a.z_page_high;
+    if (bkv == 0 && tid == 0 && a.eff) {
+      a.eff[0] = smz;
+      a.eff[1] = low ? 0.99f : 0.995f;
+    }
+  }
+
+  float tfloor[G];
+  const float* mu[G];
+  const float* sg[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int h = h0 + g;
+    mu[g] = a.mu_p + ((int64_t)b * a.H + h) * a.pages;
+    sg[g] = a.sigma_p + ((int64_t)b * a.H + h) * a.pages;
+    float s = 0.f;
+    for (int p = tid; p < a.pages; p += NT) s += fma_rn(1.5f, sg[g][p], mu[g][p]);
+    const float upper = block_sum(s, scratch) / (float)a.pages;
+    const float th = tau_hat[g];
+    const float thr = th / a.am1;
+    const float sig_delta = smz * sig_g[g];
+    const float excess = fmaxf(thr - upper, 0.0f);
+    const float tau_delta = a.frac * excess;
+    const float delta = fmaxf(sig_delta, tau_delta);
+    tfloor[g] = fma_rn(-delta, a.am1, th);
+    if (tid == 0) a.tau_floor[b * a.H + h] = tfloor[g];
+  }
+
+  const float third = 0.3333333333333333f;
+  float capmax[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) capmax[g] = -INFINITY;
+  int32_t* out = a.page_indices + b * a.pisb + kvh * a.pish;
+  int base = 0;
+  for (int c0 = 0; c0 < a.pages; c0 += NT) {
+    const int p = c0 + tid;
+    bool sel = false;
+    if (p < a.pages) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float m = mu[g][p], s = sg[g][p];
+        if (mul_rn(a.am1, fma_rn(z_page, s, m)) > tfloor[g]) sel = true;
+      }
+      if (sel) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float cap = fma_rn(mul_rn(a.z_clamp, sg[g][p]), third, mu[g][p]);
+          capmax[g] = fmaxf(capmax[g], cap);
+        }
+      }
+    }
+    int tot;
+    const int pos = block_excl_scan(sel ? 1 : 0, scan_scratch, &tot);
+    if (sel) {
+      out[base + pos] = p;
+      if (base + pos < lds_cap) lds_pages[base + pos] = p;
+    }
+    base += tot;
+  }
+  int count = base;
+  if (a.num_pages > a.pages) {
+    if (tid == 0) {
+      out[base] = a.num_pages - 1;
+      if (base < lds_cap) lds_pages[base] = a.num_pages - 1;
+    }
+    count = base + 1;
+  }
+  if (tid == 0) {
+    a.counts[bkv] = count;
+    if (a.cache_seqlens) a.cache_seqlens[bkv] = max(count - 1, 0) * a.page_size + a.last_page_size;
+  }
+  // clamp: tau = min(tau_hat, max((alpha-1) * max cap over the selection - eps, floor))
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if (a.tau_clamped) {
+      const float m = wave_max(capmax[g]);
+      if ((tid & 63) == 0) cm[tid >> 6] = m;
+      __syncthreads();
+      if (tid == 0) {
+        float mx = -INFINITY;
+        for (int w = 0; w < NT / 64; ++w) mx = fmaxf(mx, cm[w]);
+        const float th = tau_hat[g];
+        const float up = fmaxf(fma_rn(a.am1, mx, -a.eps), tfloor[g]);
+        const float tc = (mx > -3.0e38f) ? fminf(th, up) : th;
+        a.tau_clamped[b * a.H + h0 + g] = tc;
+        if (tau_out) tau_out[g] = tc;
+      }
+      __syncthreads();
+    } else if (tid == 0 && tau_out) {
+      tau_out[g] = tau_hat[g];
+    }
+  }
+  return count;
+}
+
+}  // namespace gauss
+}  // namespace ekv

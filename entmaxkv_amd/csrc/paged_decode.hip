@@ -1,746 +1,14 @@
-// Paged alpha-entmax decode over a compacted page table.
-//
-// Follows kernels/adadecode_paged.py:567-762 (exact tau: global max,
-// 16-bin histogram init, bracketed Halley, output) and
-// kernels/adadecode_paged_gaussian_tau.py:192-331 (given tau: unbounded
-// Halley/Newton corrections, output).  Compacted token c of (b, kv head) lives
-// in cache row page_indices[c / ps] * ps + c % ps; scores are
-// s_c = qs . k_c with qs = q * (alpha-1)/sqrt(D) rounded to the input dtype,
-// and out = sum_c [s_c - tau]_+^(1/(alpha-1)) v_c (not renormalised, as in
-// the reference).
-//
-// One workgroup of 1024 threads owns one (b, kv head) and all G query heads
-// of its group, so nothing crosses workgroups:
-//   phase 1  stream the selected K rows once (16-byte loads, one load serves
-//            all G heads) and keep the fp32 scores in LDS (in the workspace
-//            when they do not fit);
-//   phase 2  solve tau per head over those scores (one wave per head, or the
-//            whole workgroup per head for long token lists);
-//   phase 3  compact the tokens with s > tau (the entmax support), gather only
-//            those V rows and reduce in registers/LDS; write out.
-// When batch * kv heads is too small to fill the GPU, phase 1 runs as a
-// separate split launch over many workgroups per head (score_split_kernel)
-// and the head kernel starts at phase 2.  The reference launches 7 + 2*niter
-// kernels and reads K 3 + niter times.
-#include "ekv_common.h"
-#include "topk_device.h"
+// C entry points of the paged decode (exact / given tau), the fused top-k
+// decode step and the fused Gaussian select + decode step.  The kernels and
+// their per-(dtype, group) launchers live in decode_device.h /
+// decode_launch.h; decode_inst.hip instantiates them.
+#include "decode_device.h"
 #include "../../include/entmaxkv.h"
 
 using namespace ekv;
-
-#ifdef EKV_PHASE_TIMERS
-// experiment builds only: per-workgroup phase timestamps (wall clock, 100 MHz)
-__device__ unsigned long long ekv_phase_timers[4096 * 8];
-#define EKV_STAMP(i) \
-  if (threadIdx.x == 0 && blockIdx.x < 4096) ekv_phase_timers[blockIdx.x * 8 + (i)] = wall_clock64()
-extern "C" int ekv_debug_phase_timers(unsigned long long* host, int n) {
-  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(ekv_phase_timers), n * sizeof(unsigned long long));
-}
-__device__ unsigned long long ekv_fused_timers[4096 * 4];
-#define EKV_FSTAMP(i) \
-  if (threadIdx.x == 0 && blockIdx.x < 4096) ekv_fused_timers[blockIdx.x * 4 + (i)] = wall_clock64()
-extern "C" int ekv_debug_fused_timers(unsigned long long* host, int n) {
-  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(ekv_fused_timers), n * sizeof(unsigned long long));
-}
-#else
-#define EKV_STAMP(i)
-#define EKV_FSTAMP(i)
-#endif
+using namespace ekv::dec;
 
 namespace {
-
-constexpr int kSplitThreads = 256;
-constexpr int kSplitUnroll = 4;
-constexpr int kHeadThreads = 1024;
-constexpr int kWaves = kHeadThreads / 64;
-constexpr int kBins = 16;
-constexpr int kBatch = 8;           // independent loads per lane in score passes
-#ifndef EKV_WAVE_TAU_MAX
-#define EKV_WAVE_TAU_MAX 4096
-#endif
-constexpr int kWaveTauMax = EKV_WAVE_TAU_MAX;   // longer token lists solve tau with the whole workgroup
-constexpr int kHeadPathMinHeads = 128;
-constexpr int kTablePages = 2048;   // page ids staged in LDS per phase-1 chunk
-
-struct DecodeArgs {
-  const void* q;
-  int64_t qsb, qsh;
-  const void* k;
-  const void* v;
-  int64_t ksb, ksh, ksr;
-  int64_t row_limit;  // rows addressable in each (b, kv head) of K/V
-  const int32_t* page_indices;
-  int64_t pisb, pish;
-  int n_slots;
-  const int32_t* cache_seqlens;
-  int64_t csb, csh;
-  const int32_t* q_seqlens;
-  const float* slopes;
-  float* tau;           // [B, H] output
-  const float* tau_in;  // [B, H] starting tau (given-tau mode)
-  int tau_mode;         // 0 exact (histogram + bracketed Halley), 1 given tau (unbounded Halley)
-  int iters;
-  void* out;
-  int64_t osb, osh;
-  float alpha;
-  float qscale;  // (alpha-1)/sqrt(D) already rounded to the input dtype
-  int page_size;
-  int H, Hkv;
-  int splits;        // phase-1 workgroups per head in the split path
-  int max_tokens;    // row stride of the workspace scores
-  float* ws_scores;  // [B, H, max_tokens]
-  int stage_cap;     // scores per head kept in LDS (0: workspace)
-  int scores_ready;  // phase 1 already done by score_split_kernel
-};
-
-__device__ __forceinline__ int token_count(const DecodeArgs& a, int b, int kvh) {
-  int n = a.cache_seqlens[b * a.csb + kvh * a.csh];
-  n = max(n, 0);
-  return min(n, min(a.n_slots * a.page_size, a.max_tokens));
-}
-
-// Maps compacted token c to its cache row, or -1 when the page id is outside
-// the cache (a malformed table never causes an out-of-bounds access).
-__device__ __forceinline__ int64_t token_row(const int32_t* __restrict__ pi, int c, int ps,
-                                             int64_t row_limit) {
-  const int page = pi[c / ps];
-  const int64_t row = (int64_t)page * ps + (c % ps);
-  return (page >= 0 && row < row_limit) ? row : -1;
-}
-
-__device__ __forceinline__ float entmax_weight(float x, float alpha, float c0) {
-  if (alpha == 2.0f) return x;
-  if (alpha == 1.5f) return x * x;
-  return exp2f(log2f(x) * c0);
-}
-
-// q * qscale rounded to the storage dtype, kept in the storage format
-// (kernels/adadecode_paged.py:97-98).
-template <typename T, int G>
-__device__ __forceinline__ void load_query(const DecodeArgs& a, int b, int h0, int col,
-                                           uint4 (&qraw)[G]) {
-  constexpr int VEC = 16 / sizeof(T);
-  const T* qb = (const T*)a.q + b * a.qsb;
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    Vec<T> x;
-    x.load(qb + (h0 + g) * a.qsh + col);
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) x.v[i] = x.v[i] * a.qscale;
-    T tmp[VEC];
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) tmp[i] = from_f<T>(x.v[i]);
-    qraw[g] = *reinterpret_cast<const uint4*>(tmp);
-  }
-}
-
-// Scores of compacted tokens [c_begin, c_end) of one (b, kv head) for its G
-// heads: sc[g * stride + c].  NT threads, rows of LPR lanes, U rows per
-// segment in flight.  `pages` holds the page ids of tokens from `c_base` on
-// (LDS or global memory).
-template <typename T, int LPR, int G, int NT, int U, typename PagePtr>
-__device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, int c_begin,
-                                           int c_end, float* sc, int64_t stride, PagePtr pages,
-                                           int c_base) {
-  constexpr int VEC = 16 / sizeof(T);
-  constexpr int SEGS = NT / LPR;
-  constexpr int ROWS = SEGS * U;
-  const int seg = threadIdx.x / LPR;
-  const int sl = threadIdx.x % LPR;
-  const int col = sl * VEC;
-  const int h0 = kvh * G;
-  uint4 qraw[G];
-  load_query<T, G>(a, b, h0, col, qraw);
-  float slope[G];
-  int q_idx = 0;
-  if (a.slopes) {
-    q_idx = (a.q_seqlens ? a.q_seqlens[b] : a.cache_seqlens[b * a.csb + kvh * a.csh]) - 1;
-#pragma unroll
-    for (int g = 0; g < G; ++g) slope[g] = a.slopes[h0 + g] * (a.alpha - 1.0f);
-  }
-  const T* kh = (const T*)a.k + b * a.ksb + kvh * a.ksh;
-  const int ps = a.page_size;
-  for (int c0 = c_begin; c0 < c_end; c0 += ROWS) {
-    uint4 kv[U];
-    int rows[U];  // row within the (b, kv head); the cache holds < 2^31 rows per head
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = c0 + u * SEGS + seg;
-      rows[u] = -1;
-      if (c < c_end) {
-        const int page = pages[(c - c_base) / ps];
-        const int64_t row = (int64_t)page * ps + (c % ps);
-        rows[u] = (page >= 0 && row < a.row_limit) ? (int)row : -1;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (rows[u] >= 0) kv[u] = ld16(kh + (int64_t)rows[u] * a.ksr + col);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = c0 + u * SEGS + seg;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float acc = rows[u] >= 0 ? Dot16<T>::dot(qraw[g], kv[u], 0.f) : 0.f;
-        acc = seg_sum<LPR>(acc);
-        if (c < c_end && sl == 0) {
-          float s = acc;
-          if (rows[u] < 0) s = -INFINITY;
-          else if (a.slopes) s += slope[g] * (float)(rows[u] - q_idx);
-          sc[g * stride + c] = s;
-        }
-      }
-    }
-    if (c0 == c_begin) EKV_STAMP(2);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// tau: kernels/adadecode.py:12-112, 381-426, 555-592 and
-// kernels/adadecode_paged_gaussian_tau.py:12-53
-// ---------------------------------------------------------------------------
-
-__device__ __forceinline__ void histogram_init(const int* hist, float gmax, float alpha, float& t, float& t_lo,
-                               float& t_hi) {
-  const float t0 = gmax - 1.0f;
-  // all bins in registers first (one LDS round trip instead of one per bin)
-  int hv[kBins];
-  {
-    const int4* h4 = reinterpret_cast<const int4*>(hist);
-#pragma unroll
-    for (int j = 0; j < kBins / 4; ++j) {
-      const int4 x = h4[j];
-      hv[4 * j] = x.x;
-      hv[4 * j + 1] = x.y;
-      hv[4 * j + 2] = x.z;
-      hv[4 * j + 3] = x.w;
-    }
-  }
-  if (alpha == 2.0f || alpha == 1.5f) {
-    float sum_z = 1.f, sum_k = 1.f, sum_z2 = 1.f;
-#pragma unroll
-    for (int sj = kBins - 1; sj >= 0; --sj) {
-      float c_bin = (float)hv[sj];
-      if (sj == kBins - 1) c_bin -= 1.0f;
-      const float c_tau = (float)sj / (float)kBins;
-      const float new_z = sum_z + c_bin * c_tau;
-      const float new_k = sum_k + c_bin;
-      if (alpha == 2.0f) {
-        if ((new_z - new_k * c_tau) < 1.0f) {
-          sum_z = new_z;
-          sum_k = new_k;
-        }
-      } else {
-        const float new_z2 = sum_z2 + c_bin * (c_tau * c_tau);
-        if (new_k * c_tau * c_tau - 2.0f * new_z * c_tau + new_z2 < 1.0f) {
-          sum_z = new_z;
-          sum_k = new_k;
-          sum_z2 = new_z2;
-        }
-      }
-    }
-    float t_init;
-    if (alpha == 2.0f) {
-      t_init = gmax + (sum_z - 1.0f) / sum_k - 1.0f;
-    } else {
-      const float disc = sum_z * sum_z - sum_k * (sum_z2 - 1.0f);
-      t_init = gmax + (sum_z - sqrtf(disc)) / sum_k - 1.0f;
-    }
-    t_lo = t_init;
-    t_hi = t_init + 1.0f / kBins;
-  } else {
-    const float p = 1.0f / (alpha - 1.0f);
-    int lo = 0, hi = kBins - 1, found = 0, b_idx = 0;
-    for (int it = 0; it < 5; ++it) {
-      const int mid = (int)((float)(lo + hi) * 0.5f);
-      float fL = 0.f, fU = 0.f;
-#pragma unroll
-      for (int j = 0; j < kBins; ++j) {
-        const int off = j - mid;
-        if (off < 0) continue;
-        float cnt = (float)hv[j];
-        if (j == kBins - 1) cnt -= 1.0f;
-        const float zL = (float)off / kBins;
-        const float zU = ((float)off + 1.0f) / kBins;
-        if (zL > 0.f) fL += cnt * exp2f(log2f(zL) * p);
-        fU += cnt * exp2f(log2f(zU) * p);
-      }
-      fL -= 1.0f;
-      fU -= 1.0f;
-      const bool go_right = fL > 0.f, go_left = fU < 0.f;
-      const bool bracket = !go_right && !go_left;
-      if (found == 0) {
-        if (bracket) {
-          b_idx = mid;
-          found = 1;
-        }
-        if (go_right) lo = mid + 1;
-        if (go_left) hi = mid - 1;
-      }
-    }
-    const int b_sel = found ? b_idx : min(lo, kBins - 1);
-    t_lo = t0 + (float)b_sel / kBins;
-    t_hi = t0 + (float)min(b_sel + 1, kBins) / kBins;
-  }
-  t = 0.5f * (t_lo + t_hi);
-}
-
-__device__ __forceinline__ void halley_bisect(float& t, float& t_lo, float& t_hi, float a0,
-                                              float a1, float a2, float c0, float c1) {
-  const float ff = a0 - 1.0f;
-  const float df = -c0 * a1;
-  const float ddf = c0 * c1 * a2;
-  if (ff > 0.f) t_lo = t;
-  if (ff < 0.f) t_hi = t;
-  const float new_t = t - (2.f * ff * df) / (2.f * df * df - ff * ddf);
-  const bool good = (new_t > t_lo - 1e-6f) && (new_t < t_hi + 1e-6f);
-  t = good ? new_t : 0.5f * (t_lo + t_hi);
-}
-
-__device__ __forceinline__ float halley_unbounded(float t, float a0, float a1, float a2, float c0,
-                                                  float c1) {
-  const float ff = a0 - 1.0f;
-  const float df = -c0 * a1;
-  const float ddf = c0 * c1 * a2;
-  const float hden = 2.0f * df * df - ff * ddf;
-  float tn;
-  if (fabsf(hden) > 1e-12f) tn = t - (2.0f * ff * df) / hden;
-  else if (fabsf(df) > 1e-12f) tn = t - ff / df;
-  else tn = t;
-  if (!(tn == tn && fabsf(tn) < 1e20f)) tn = t;
-  return tn;
-}
-
-// Reduction scope of a tau solve: a team of W consecutive waves owns one head
-// (lanes stride 64 * W).  W = 1 needs no workgroup barrier; for W > 1 every
-// wave of the workgroup makes the same sequence of reductions (a wave without
-// a head runs the solve on zero scores), and the partials of each reduction
-// go through one of two LDS buffers in turn, so one barrier per reduction
-// suffices.
-template <int W>
-struct TeamScope {
-  static constexpr int kStride = 64 * W;
-  float4* part;  // [2][kWaves] per-wave partials (LDS)
-  int wid, lane, team, pos, parity;
-  __device__ __forceinline__ TeamScope(float4* p) : part(p), parity(0) {
-    wid = threadIdx.x >> 6;
-    lane = threadIdx.x & 63;
-    team = wid / W;
-    pos = wid % W;
-  }
-  __device__ __forceinline__ int first() const { return pos * 64 + lane; }
-  __device__ __forceinline__ void sync() const {
-    if constexpr (W == 1) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    } else {
-      __syncthreads();
-    }
-  }
-  __device__ __forceinline__ float max(float x) {
-    x = wave_max(x);
-    if constexpr (W > 1) {
-      float4* buf = part + parity * kWaves;
-      if (lane == 0) buf[wid].x = x;
-      __syncthreads();
-      x = buf[team * W].x;
-#pragma unroll
-      for (int w = 1; w < W; ++w) x = fmaxf(x, buf[team * W + w].x);
-      parity ^= 1;
-    }
-    return x;
-  }
-  __device__ __forceinline__ void sum3(float& a, float& b, float& c) {
-    a = wave_sum(a);
-    b = wave_sum(b);
-    c = wave_sum(c);
-    if constexpr (W > 1) {
-      float4* buf = part + parity * kWaves;
-      if (lane == 0) buf[wid] = make_float4(a, b, c, 0.f);
-      __syncthreads();
-      float4 r = buf[team * W];
-#pragma unroll
-      for (int w = 1; w < W; ++w) {
-        const float4 y = buf[team * W + w];
-        r.x += y.x;
-        r.y += y.y;
-        r.z += y.z;
-      }
-      a = r.x;
-      b = r.y;
-      c = r.z;
-      parity ^= 1;
-    }
-  }
-};
-
-// One pass over scores[0..n) of a head: the sums of [s - t]_+^(1/(alpha-1) - j)
-// for j = 0, 1, 2 (kernels/adadecode_paged.py:357-372), branch-free per score.
-template <typename S>
-__device__ __forceinline__ void accumulate_pass(S& sp, const float* __restrict__ sc, int n, float t,
-                                                float alpha, float c0, float& a0, float& a1,
-                                                float& a2) {
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f;
-  const bool generic = !(alpha == 2.0f || alpha == 1.5f);
-  const bool sparsemax = alpha == 2.0f;
-  for (int b0 = 0; b0 < n; b0 += S::kStride * kBatch) {
-    float x[kBatch];
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int c = b0 + j * S::kStride + sp.first();
-      x[j] = c < n ? sc[c] : -INFINITY;
-    }
-    if (!generic) {
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const bool act = x[j] > t;
-        const float d = act ? x[j] - t : 0.f;
-        const float one = act ? 1.f : 0.f;
-        s0 += sparsemax ? d : d * d;
-        s1 += sparsemax ? one : d;
-        s2 += sparsemax ? 0.f : one;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        if (x[j] > t) {
-          const float l = log2f(x[j] - t);
-          s0 += exp2f(l * c0);
-          s1 += exp2f(l * (c0 - 1.f));
-          s2 += exp2f(l * (c0 - 2.f));
-        }
-      }
-    }
-  }
-  sp.sum3(s0, s1, s2);
-  a0 = s0;
-  a1 = s1;
-  a2 = s2;
-}
-
-// tau of one head (kernels/adadecode_paged.py:140-247, 357-372 and
-// kernels/adadecode_paged_gaussian_tau.py:12-53).  `hist` (kBins ints, LDS)
-// must be zero on entry when tau_mode is 0.
-template <typename S>
-__device__ __forceinline__ float solve_tau(S& sp, const DecodeArgs& a, const float* __restrict__ sc,
-                                           int n, float tau_in, int* hist) {
-  const float alpha = a.alpha;
-  const float c0 = 1.0f / (alpha - 1.0f);
-  const float c1 = c0 - 1.0f;
-  float t;
-  if (a.tau_mode == 0) {
-    float m = -1.0e6f;
-    for (int b0 = 0; b0 < n; b0 += S::kStride * kBatch) {
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int c = b0 + j * S::kStride + sp.first();
-        if (c < n) m = fmaxf(m, sc[c]);
-      }
-    }
-    const float gmax = sp.max(m);
-    EKV_STAMP(4);
-    const float t0 = gmax - 1.0f;
-    for (int b0 = 0; b0 < n; b0 += S::kStride * kBatch) {
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int c = b0 + j * S::kStride + sp.first();
-        if (c < n) {
-          const float f = (sc[c] - t0) * (float)kBins;
-          if (f > -1.0f) atomicAdd(&hist[min((int)f, kBins - 1)], 1);
-        }
-      }
-    }
-    sp.sync();
-    float t_lo, t_hi;
-    EKV_STAMP(5);
-    histogram_init(hist, gmax, alpha, t, t_lo, t_hi);
-    for (int it = 0; it < a.iters; ++it) {
-      float a0, a1, a2;
-      accumulate_pass(sp, sc, n, t, alpha, c0, a0, a1, a2);
-      halley_bisect(t, t_lo, t_hi, a0, a1, a2, c0, c1);
-    }
-  } else {
-    t = tau_in;
-    for (int it = 0; it < a.iters; ++it) {
-      float a0, a1, a2;
-      accumulate_pass(sp, sc, n, t, alpha, c0, a0, a1, a2);
-      t = halley_unbounded(t, a0, a1, a2, c0, c1);
-    }
-  }
-  return t;
-}
-
-// ---------------------------------------------------------------------------
-// phase 1 as its own launch (few heads)
-// ---------------------------------------------------------------------------
-
-template <typename T, int LPR, int G>
-__global__ __launch_bounds__(kSplitThreads) void score_split_kernel(DecodeArgs a) {
-  const int split = blockIdx.x;
-  const int bkv = blockIdx.y;
-  const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
-  const int n = token_count(a, b, kvh);
-  const int per = (n + a.splits - 1) / a.splits;
-  const int c_start = split * per;
-  const int c_end = min(c_start + per, n);
-  if (c_start >= c_end) return;
-  float* sc = a.ws_scores + ((int64_t)b * a.H + kvh * G) * a.max_tokens;
-  const int32_t* pi = a.page_indices + b * a.pisb + kvh * a.pish;
-  score_rows<T, LPR, G, kSplitThreads, kSplitUnroll>(a, b, kvh, c_start, c_end, sc, a.max_tokens,
-                                                     pi, 0);
-}
-
-// ---------------------------------------------------------------------------
-// the head kernel
-// ---------------------------------------------------------------------------
-
-struct HeadShared {
-  int (*hist)[kBins];
-  float4* part;  // [2][kWaves] reduction partials
-  float* s_tau;
-  int64_t* sup_row;
-  float* sup_p;  // [G][kHeadThreads]
-  int* flag_cnt;
-  float* red;    // [kWaves][D]
-  int* s_pages;  // [kTablePages]
-};
-
-// tau of the G heads of one (b, kv head): head g is solved by the team of W
-// waves g * W .. g * W + W - 1 (short token lists: W = 4 / G, one wave per
-// SIMD; long ones: every wave of the workgroup).
-template <int W, int G>
-__device__ __forceinline__ void solve_heads(const DecodeArgs& a, int b, int h0, int n,
-                                            const float* sc, int64_t stride,
-                                            const HeadShared& sh) {
-  TeamScope<W> sp(sh.part);
-  const int g = sp.team;
-  if (W == 1 && g >= G) return;
-  const bool real = g < G;
-  const float tin = (real && a.tau_mode == 1) ? a.tau_in[b * a.H + h0 + g] : 0.f;
-  const float t = solve_tau(sp, a, sc + (real ? g : 0) * stride, real ? n : 0, tin, sh.hist[g]);
-  if (real && sp.pos == 0 && sp.lane == 0) sh.s_tau[g] = t;
-}
-
-// Phases 1-3 of one (b, kv head); `sc` points to LDS when kStaged (so every
-// score access is a ds_* instruction) and to the workspace otherwise.
-template <typename T, int LPR, int G, int U, bool kStaged, bool kTableInLds = false>
-__device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int kvh, int n,
-                                                 float* sc, int64_t stride, const HeadShared& sh) {
-  constexpr int VEC = 16 / sizeof(T);
-  constexpr int SEGS = kHeadThreads / LPR;
-  constexpr int D = LPR * VEC;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wid = tid >> 6;
-  const int h0 = kvh * G;
-  const int ps = a.page_size;
-  const int32_t* pi = a.page_indices + b * a.pisb + kvh * a.pish;
-
-  EKV_STAMP(0);
-  if (tid < kWaves * kBins) (&sh.hist[0][0])[tid] = 0;  // read after the phase-1 barriers
-  // phase 1: scores, the page table staged in LDS chunk by chunk
-  if (kTableInLds) {
-    // the whole page table is already in sh.s_pages (written by this workgroup)
-    score_rows<T, LPR, G, kHeadThreads, U>(a, b, kvh, 0, n, sc, stride, sh.s_pages, 0);
-  } else if (!a.scores_ready) {
-    for (int cb = 0; cb < n; cb += kTablePages * ps) {
-      const int ce = min(n, cb + kTablePages * ps);
-      const int np = (ce - cb + ps - 1) / ps;
-      for (int i = tid; i < np; i += kHeadThreads) sh.s_pages[i] = pi[cb / ps + i];
-      __syncthreads();
-      EKV_STAMP(1);
-      score_rows<T, LPR, G, kHeadThreads, U>(a, b, kvh, cb, ce, sc, stride, sh.s_pages, cb);
-      __syncthreads();
-    }
-  }
-  __syncthreads();
-  EKV_STAMP(3);
-
-  // phase 2: tau per head, one team of waves per head
-  if (n <= kWaveTauMax) {
-    solve_heads<(G >= 4 ? 1 : 4 / G), G>(a, b, h0, n, sc, stride, sh);
-  } else {
-    solve_heads<kWaves / G, G>(a, b, h0, n, sc, stride, sh);
-  }
-  __syncthreads();
-  float tau[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) tau[g] = sh.s_tau[g];
-  if (tid < G) a.tau[b * a.H + h0 + tid] = sh.s_tau[tid];
-  EKV_STAMP(6);
-
-  // phase 3: gather the support's V rows
-  const float alpha = a.alpha;
-  const float c0 = 1.0f / (alpha - 1.0f);
-  const int seg = tid / LPR;
-  const int col = (tid % LPR) * VEC;
-  const T* vh = (const T*)a.v + b * a.ksb + kvh * a.ksh;
-  float acc[G][VEC];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) acc[g][i] = 0.f;
-
-  for (int t0 = 0; t0 < n; t0 += kHeadThreads) {
-    const int c = t0 + tid;
-    float p[G];
-    bool any = false;
-    int64_t row = -1;
-    if (c < n) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float s = sc[g * stride + c];
-        p[g] = 0.f;
-        if (s > tau[g]) {
-          p[g] = entmax_weight(s - tau[g], alpha, c0);
-          any = true;
-        }
-      }
-      if (any) {
-        row = token_row(kTableInLds ? sh.s_pages : pi, c, ps, a.row_limit);
-        if (row < 0) any = false;
-      }
-    }
-    const uint64_t m = __ballot(any);
-    if (lane == 0) sh.flag_cnt[wid] = __popcll(m);
-    __syncthreads();
-    int before = 0, nsup = 0;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const int cw = sh.flag_cnt[w];
-      before += (w < wid) ? cw : 0;
-      nsup += cw;
-    }
-    if (any) {
-      const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-      const int slot = before + __popcll(m & below);
-      sh.sup_row[slot] = row;
-#pragma unroll
-      for (int g = 0; g < G; ++g) sh.sup_p[g * kHeadThreads + slot] = p[g];
-    }
-    __syncthreads();
-    for (int j0 = seg; j0 < nsup; j0 += 2 * SEGS) {
-      const int j1 = j0 + SEGS;
-      Vec<T> x0, x1;
-      x0.load(vh + sh.sup_row[j0] * a.ksr + col);
-      if (j1 < nsup) x1.load(vh + sh.sup_row[j1] * a.ksr + col);
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float w0 = sh.sup_p[g * kHeadThreads + j0];
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[g][i] += w0 * x0.v[i];
-        if (j1 < nsup) {
-          const float w1 = sh.sup_p[g * kHeadThreads + j1];
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) acc[g][i] += w1 * x1.v[i];
-        }
-      }
-    }
-    __syncthreads();
-  }
-  EKV_STAMP(7);
-
-  // reduce the row segments: within each wave by shuffles, then across waves
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      acc[g][i] = lanes::cross_seg_sum<LPR>(acc[g][i]);
-    }
-    if (lane < LPR) {
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) sh.red[wid * D + col + i] = acc[g][i];
-    }
-    __syncthreads();
-    for (int e = tid; e < D; e += kHeadThreads) {
-      float r = 0.f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) r += sh.red[w * D + e];
-      T* o = (T*)a.out + b * a.osb + (h0 + g) * a.osh;
-      o[e] = from_f<T>(r);
-    }
-    __syncthreads();
-  }
-}
-
-template <typename T, int LPR, int G, int U>
-__global__ __launch_bounds__(kHeadThreads) void decode_head_kernel(DecodeArgs a) {
-  constexpr int VEC = 16 / sizeof(T);
-  constexpr int D = LPR * VEC;
-  extern __shared__ float stage[];  // [G][stage_cap] scores when staged
-  __shared__ __attribute__((aligned(16))) int hist[kWaves][kBins];
-  __shared__ float4 part[2 * kWaves];
-  __shared__ float s_tau[G];
-  __shared__ int64_t sup_row[kHeadThreads];
-  __shared__ float sup_p[G * kHeadThreads];
-  __shared__ int flag_cnt[kWaves];
-  __shared__ float red[kWaves * D];
-  __shared__ int s_pages[kTablePages];
-  const HeadShared sh{hist, part, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
-
-  const int bkv = blockIdx.x;
-  const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
-  const int n = token_count(a, b, kvh);
-  if (!a.scores_ready && n <= a.stage_cap) {
-    decode_head_body<T, LPR, G, U, true>(a, b, kvh, n, stage, a.stage_cap, sh);
-  } else {
-    float* ws = a.ws_scores + ((int64_t)b * a.H + kvh * G) * a.max_tokens;
-    decode_head_body<T, LPR, G, U, false>(a, b, kvh, n, ws, a.max_tokens, sh);
-  }
-}
-
-// Criticality scan + top-k page selection of one step, as read by the fused
-// kernel (see ekv_topk_paged_entmax_decode).
-struct SelectArgs {
-  const void* kmin;
-  const void* kmax;
-  int64_t ssb, ssh, ssp;
-  void* scores;       // [B, H, num_pages] query dtype
-  int num_pages;      // pages scored (the last, partial page excluded)
-  int seq_len, q_pos;
-  int k;              // pages selected per (b, kv head)
-  int last_page;      // appended at slot k (the sentinel), or -1
-  int key_cap;        // page keys that fit the dynamic LDS
-};
-
-// One (b, kv head) per workgroup end to end: criticality scan of every page,
-// top-k (page table to global memory and to LDS), then phases 1-3 of the
-// decode on the selected pages.  Keys and then scores share the dynamic LDS.
-template <typename T, int LPR, int G, int UC, int UD>
-__global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a, SelectArgs t) {
-  constexpr int VEC = 16 / sizeof(T);
-  constexpr int D = LPR * VEC;
-  extern __shared__ float stage[];
-  __shared__ __attribute__((aligned(16))) int hist[kWaves][kBins];
-  __shared__ float4 part[2 * kWaves];
-  __shared__ float s_tau[G];
-  __shared__ int64_t sup_row[kHeadThreads];
-  __shared__ float sup_p[G * kHeadThreads];
-  __shared__ int flag_cnt[kWaves];
-  __shared__ float red[kWaves * D];
-  __shared__ int s_pages[kTablePages];
-  const HeadShared sh{hist, part, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
-
-  const int bkv = blockIdx.x;
-  const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
-  uint32_t* keys = reinterpret_cast<uint32_t*>(stage);
-  const bool keep = t.num_pages <= t.key_cap;
-  EKV_FSTAMP(0);
-  const T* sbase = topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC>(
-      (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
-      a.slopes, (T*)t.scores, a.H, t.num_pages, a.page_size, t.seq_len, t.q_pos, b, kvh,
-      keep ? keys : nullptr);
-  __syncthreads();
-  EKV_FSTAMP(1);
-  int32_t* pi = const_cast<int32_t*>(a.page_indices) + b * a.pisb + kvh * a.pish;
-  topk::topk_select_block<T, G, kHeadThreads>(sbase, t.num_pages, t.num_pages, t.k, t.last_page,
-                                              pi, keys, keep ? t.num_pages : 0, keep, s_pages);
-  __syncthreads();
-  EKV_FSTAMP(2);
-  const int n = token_count(a, b, kvh);
-  decode_head_body<T, LPR, G, UD, true, true>(a, b, kvh, n, stage, a.stage_cap, sh);
-  EKV_FSTAMP(3);
-}
 
 template <typename F>
 int dispatch_group(int G, F&& f) {
@@ -798,10 +66,6 @@ DecodeArgs make_decode_args(
   return a;
 }
 
-// LDS per workgroup on gfx950, and the part of it given to staged scores.
-constexpr int kLdsPerWorkgroup = 160 * 1024;
-constexpr int kStageBytes = 96 * 1024;
-
 }  // namespace
 
 extern "C" int64_t ekv_decode_workspace_bytes(int B, int H, int Hkv, int D, int splits,
@@ -846,39 +110,8 @@ extern "C" int ekv_paged_entmax_decode(
   a.scores_ready = head_path ? 0 : 1;
   return dispatch_dtype(dtype, [&](auto tv) {
     using T = decltype(tv);
-    return dispatch_lpr<T>(D, [&](auto lpr) {
-      constexpr int LPR = decltype(lpr)::value;
-      return dispatch_group(G, [&](auto gv) {
-        constexpr int GG = decltype(gv)::value;
-        constexpr int U = GG >= 4 ? 2 : 8 / GG;
-        if (!head_path) {
-          hipLaunchKernelGGL((score_split_kernel<T, LPR, GG>), dim3(splits, B * Hkv),
-                             dim3(kSplitThreads), 0, s, a);
-          int rc = check_launch("score_split_kernel");
-          if (rc) return rc;
-        }
-        auto kern = decode_head_kernel<T, LPR, GG, U>;
-        if (a.stage_cap > 0) {
-          // LDS left for staged scores next to the kernel's static LDS
-          hipFuncAttributes attr;
-          hipError_t e = hipFuncGetAttributes(&attr, (const void*)kern);
-          if (e != hipSuccess)
-            return set_error(EKV_ERR_HIP, "decode_head_kernel attributes: %s", hipGetErrorString(e));
-          const int64_t avail = (int64_t)kLdsPerWorkgroup - (int64_t)attr.sharedSizeBytes;
-          const int64_t fit = avail > 0 ? avail / (4 * GG) : 0;
-          if (fit < a.stage_cap) a.stage_cap = (int)fit;
-        }
-        const size_t lds = (size_t)a.stage_cap * GG * sizeof(float);
-        if (lds > 0) {
-          hipError_t e = hipFuncSetAttribute((const void*)kern,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-          if (e != hipSuccess)
-            return set_error(EKV_ERR_HIP, "decode_head_kernel LDS %zu: %s", lds,
-                             hipGetErrorString(e));
-        }
-        hipLaunchKernelGGL(kern, dim3(B * Hkv), dim3(kHeadThreads), lds, s, a);
-        return check_launch("decode_head_kernel");
-      });
+    return dispatch_group(G, [&](auto gv) {
+      return dec::Launch<T, decltype(gv)::value>::decode(a, B, Hkv, D, head_path, s);
     });
   });
 }
@@ -950,32 +183,122 @@ extern "C" int ekv_topk_paged_entmax_decode(
   int handled = 0;
   const int rc = dispatch_dtype(dtype, [&](auto tv) {
     using T = decltype(tv);
-    return dispatch_lpr<T>(D, [&](auto lpr) {
-      constexpr int LPR = decltype(lpr)::value;
-      return dispatch_group(G, [&](auto gv) {
-        constexpr int GG = decltype(gv)::value;
-        constexpr int UC = GG >= 8 ? 1 : (GG == 1 ? 4 : 8 / GG);
-        constexpr int UD = GG >= 4 ? 2 : 8 / GG;
-        auto kern = topk_decode_kernel<T, LPR, GG, UC, UD>;
-        hipFuncAttributes attr;
-        hipError_t e = hipFuncGetAttributes(&attr, (const void*)kern);
-        if (e != hipSuccess)
-          return set_error(EKV_ERR_HIP, "topk_decode_kernel attributes: %s", hipGetErrorString(e));
-        const int64_t keys = (int64_t)num_pages * 4;
-        const int64_t stage = (int64_t)tokens * GG * 4;
-        const int64_t lds = keys > stage ? keys : stage;
-        if ((int64_t)attr.sharedSizeBytes + lds > kLdsPerWorkgroup) return 0;  // too big: fall back
-        e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds);
-        if (e != hipSuccess)
-          return set_error(EKV_ERR_HIP, "topk_decode_kernel LDS %lld: %s", (long long)lds,
-                           hipGetErrorString(e));
-        hipLaunchKernelGGL(kern, dim3(B * Hkv), dim3(kHeadThreads), (size_t)lds, s, a, t);
-        handled = 1;
-        return check_launch("topk_decode_kernel");
-      });
+    return dispatch_group(G, [&](auto gv) {
+      return dec::Launch<T, decltype(gv)::value>::topk(a, t, B, Hkv, D, tokens, s, &handled);
     });
   });
   if (rc || handled) return rc;
   return two_launches();
+}
+
+extern "C" int ekv_gaussian_paged_entmax_decode(
+    const void* moments_workspace, int64_t moments_workspace_bytes, const float* mu_p,
+    const float* sigma_p, int pages_for_stats, int num_pages, float* mu_g, float* sigma_g,
+    float* mean_var, float* var_means, float* tau_hat, int tau_hat_given, int n_tokens,
+    int tau_iters, float tol, int auto_margins, float safety_margin_z, float z_page,
+    float z_page_low, float z_page_high, float threshold_excess_margin_fraction,
+    int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h, int32_t* counts,
+    float* tau_floor, int32_t* cache_seqlens, int last_page_size, float* tau_clamped,
+    float z_clamp, float eps, float* effective_margins, const void* q, int64_t q_stride_b,
+    int64_t q_stride_h, const void* k, const void* v, int64_t kv_stride_b, int64_t kv_stride_h,
+    int64_t kv_stride_row, int64_t kv_rows, const int32_t* q_seqlens, const float* alibi_slopes,
+    float* tau, int tau_mode, int iters, void* out, int64_t out_stride_b, int64_t out_stride_h,
+    float alpha, float qscale, int page_size, int B, int H, int Hkv, int D, int max_tokens,
+    void* workspace, int64_t workspace_bytes, int dtype, void* stream) {
+  EKV_REQUIRE(moments_workspace && mu_p && sigma_p && mu_g && sigma_g && mean_var && var_means &&
+                  tau_hat && page_indices && counts && tau_floor && cache_seqlens && q && k &&
+                  v && tau && out && workspace,
+              "ekv_gaussian_paged_entmax_decode: null pointer");
+  EKV_REQUIRE(B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0,
+              "ekv_gaussian_paged_entmax_decode: bad heads");
+  EKV_REQUIRE(pages_for_stats > 0 && num_pages >= pages_for_stats && page_size > 0,
+              "ekv_gaussian_paged_entmax_decode: bad page counts");
+  EKV_REQUIRE(moments_workspace_bytes >=
+                  ekv_gaussian_workspace_bytes(B, H, Hkv, D, pages_for_stats, dtype),
+              "ekv_gaussian_paged_entmax_decode: moments workspace too small");
+  EKV_REQUIRE(tau_hat_given || alpha == 2.0f || alpha == 1.5f || fabsf(alpha - 4.0f / 3.0f) < 1e-6f,
+              "ekv_gaussian_paged_entmax_decode: tau-hat needs alpha in {2, 1.5, 4/3}");
+  EKV_REQUIRE(tau_mode == 0 || tau_mode == 1, "ekv_gaussian_paged_entmax_decode: tau_mode %d",
+              tau_mode);
+  EKV_REQUIRE(iters >= 0 && max_tokens >= num_pages * page_size,
+              "ekv_gaussian_paged_entmax_decode: bad decode parameters");
+  EKV_REQUIRE(workspace_bytes >= ekv_decode_workspace_bytes(B, H, Hkv, D, 1, max_tokens),
+              "ekv_gaussian_paged_entmax_decode: workspace too small");
+  hipStream_t s = (hipStream_t)stream;
+  const int G = H / Hkv;
+  const float* tau_start = tau_clamped ? tau_clamped : tau_hat;
+  if (B * Hkv < kHeadPathMinHeads) {
+    // few heads: moments, selection and a split decode as separate launches
+    int rc = gauss::launch_finalize(moments_workspace, B, H, Hkv, pages_for_stats, mu_g, sigma_g,
+                                    mean_var, var_means, tau_hat_given ? nullptr : tau_hat, alpha,
+                                    n_tokens, tau_iters, tol, s);
+    if (rc) return rc;
+    rc = ekv_select_gaussian_pack(mu_p, sigma_p, tau_hat, sigma_g, B, H, Hkv, pages_for_stats,
+                                  num_pages, alpha, auto_margins, safety_margin_z, z_page,
+                                  z_page_low, z_page_high, threshold_excess_margin_fraction,
+                                  page_indices, pi_stride_b, pi_stride_h, counts, tau_floor,
+                                  cache_seqlens, page_size, last_page_size, tau_clamped, z_clamp,
+                                  eps, effective_margins, stream);
+    if (rc) return rc;
+    return ekv_paged_entmax_decode(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h,
+                                   kv_stride_row, kv_rows, page_indices, pi_stride_b, pi_stride_h,
+                                   num_pages, cache_seqlens, Hkv, 1, q_seqlens, alibi_slopes,
+                                   tau_start, tau, tau_mode, iters, out, out_stride_b,
+                                   out_stride_h, alpha, qscale, page_size, B, H, Hkv, D, 1,
+                                   max_tokens, workspace, workspace_bytes, dtype, stream);
+  }
+  DecodeArgs a = make_decode_args(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h,
+                                  kv_stride_row, kv_rows, page_indices, pi_stride_b, pi_stride_h,
+                                  num_pages, cache_seqlens, Hkv, 1, q_seqlens, alibi_slopes,
+                                  tau_start, tau, tau_mode, iters, out, out_stride_b,
+                                  out_stride_h, alpha, qscale, page_size, H, Hkv, 1, max_tokens,
+                                  workspace);
+  a.scores_ready = 0;
+  GaussArgs f;
+  gauss::SelectArgs& sel = f.sel;
+  sel.mu_p = mu_p;
+  sel.sigma_p = sigma_p;
+  sel.B = B;
+  sel.H = H;
+  sel.Hkv = Hkv;
+  sel.pages = pages_for_stats;
+  sel.num_pages = num_pages;
+  sel.am1 = (float)(alpha - 1.0);
+  sel.auto_margins = auto_margins;
+  sel.smz = safety_margin_z;
+  sel.z_page = z_page;
+  sel.z_page_low = z_page_low;
+  sel.z_page_high = z_page_high;
+  sel.frac = threshold_excess_margin_fraction;
+  sel.page_indices = page_indices;
+  sel.pisb = pi_stride_b;
+  sel.pish = pi_stride_h;
+  sel.counts = counts;
+  sel.tau_floor = tau_floor;
+  sel.cache_seqlens = cache_seqlens;
+  sel.page_size = page_size;
+  sel.last_page_size = last_page_size;
+  sel.tau_clamped = tau_clamped;
+  sel.z_clamp = z_clamp;
+  sel.eps = eps;
+  sel.eff = effective_margins;
+  f.partials = (const float4*)moments_workspace;
+  f.splits = gauss::moment_splits(B * Hkv, pages_for_stats);
+  f.mu_g = mu_g;
+  f.sigma_g = sigma_g;
+  f.mean_var = mean_var;
+  f.var_means = var_means;
+  f.tau_hat = tau_hat;
+  f.tau_hat_given = tau_hat_given;
+  f.tau_alpha = fabsf(alpha - 4.0f / 3.0f) < 1e-6f ? 4.0f / 3.0f : alpha;
+  f.n_tokens = (float)n_tokens;
+  f.log_n_factor = (float)sqrt(2.0 * log((double)n_tokens + 1.0));
+  f.tau_iters = tau_iters;
+  f.tol = tol;
+  return dispatch_dtype(dtype, [&](auto tv) {
+    using T = decltype(tv);
+    return dispatch_group(G, [&](auto gv) {
+      return dec::Launch<T, decltype(gv)::value>::gaussian(a, f, B, Hkv, D, max_tokens, s);
+    });
+  });
 }

@@ -4,8 +4,9 @@ Differences from the reference, all on the host side:
 * the automatic ``safety_margin_z``/``max_quantile`` (gaussian_utils.py:163-169)
   are derived on the device inside the selection launch, so no ``.item()``
   synchronisation happens per decode step; the dict carries None for them;
-* tau-hat is solved inside the statistics launch (single Gaussian) or by one
-  extra launch (page mixture, ALiBi only).
+* tau-hat is solved on the device right after the global moments (single
+  Gaussian, one wave per head) or by one extra launch (page mixture, ALiBi
+  only).
 """
 
 from __future__ import annotations
@@ -56,6 +57,16 @@ def compute_gaussian_aware_statistics(q, k_mean, k_std, seq_len: int, page_size:
         tau_hat = solve_for_tau_hat_page_gaussian_mixture_auto(
             buf.mu_p, buf.sigma_p, alpha=alpha, uniform_page_count=float(page_size))
         buf.tau_hat.copy_(tau_hat.squeeze(-1))
+    return stats_dict(buf, seq_len_for_stats, pages_for_stats, num_pages,
+                      threshold_excess_margin_fraction, tau_clamp_page_max_quantile,
+                      safety_margin_z, max_quantile)
+
+
+def stats_dict(buf, seq_len_for_stats: int, pages_for_stats: int, num_pages: int,
+               threshold_excess_margin_fraction: float, tau_clamp_page_max_quantile: float,
+               safety_margin_z=None, max_quantile=None) -> dict:
+    """The reference's statistics dict (gaussian_utils.py:183-200) over the
+    device buffers of one step."""
     return {
         "mu_scores_per_page": buf.mu_p,
         "sigma_scores_per_page": buf.sigma_p,

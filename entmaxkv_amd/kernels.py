@@ -396,6 +396,96 @@ def compute_page_gaussian_stats(q, k_mean, k_std, pages_for_stats, *, alibi_slop
     return buffers
 
 
+def _alibi_f32(alibi_slopes, device):
+    if alibi_slopes is None:
+        return None
+    slopes = alibi_slopes.to(device=device, dtype=torch.float32)
+    if slopes.dim() == 2:
+        slopes = slopes[0]
+    return slopes.contiguous()
+
+
+def compute_page_gaussian_moments(q, k_mean, k_std, pages_for_stats, buffers: GaussianBuffers, *,
+                                  alibi_slopes=None, page_size=16, seq_len=0,
+                                  n_tokens=None) -> GaussianBuffers:
+    """Per-page moments mu_p / sigma_p and the partial sums of the global moments
+    (the first launch of the Gaussian step; kernels/gaussian_page_stats.py:8-121)."""
+    require_gpu(q, k_mean, k_std)
+    B, H, _, D = q.shape
+    Hkv = k_mean.shape[1]
+    if buffers.spec != (B, H, Hkv, D, pages_for_stats, q.dtype, q.device):
+        raise ValueError(f"Gaussian buffers {buffers.spec} do not match the step")
+    if k_mean.stride() != k_std.stride():
+        raise ValueError("k_mean and k_std must share strides")
+    if n_tokens is None:
+        n_tokens = pages_for_stats * page_size
+    q3 = _row_major_d(q[:, :, 0], "q")
+    call("ekv_gaussian_moments", q3.data_ptr(), q3.stride(0), q3.stride(1), k_mean.data_ptr(),
+         k_std.data_ptr(), k_mean.stride(0), k_mean.stride(1), k_mean.stride(2), pages_for_stats,
+         ptr(_alibi_f32(alibi_slopes, q.device)), page_size, seq_len, int(n_tokens),
+         buffers.mu_p.data_ptr(), buffers.sigma_p.data_ptr(), B, H, Hkv, D, buffers.ws.data_ptr(),
+         buffers.ws.numel(), dtype_code(q.dtype), stream_ptr(q.device))
+    return buffers
+
+
+def gaussian_paged_entmax_decode(q, k_cache, v_cache, out, buffers: GaussianBuffers, *,
+                                 pages_for_stats: int, num_pages: int, n_tokens: int,
+                                 page_size: int, alpha: float, tau_hat_given: bool,
+                                 safety_margin_z, max_quantile,
+                                 threshold_excess_margin_fraction: float, page_indices, counts,
+                                 tau_floor, cache_seqlens, last_page_size: int, tau_clamped,
+                                 clamp_quantile: float, effective, tau_out, tau_mode: int,
+                                 iters: int, workspace: DecodeWorkspace, alibi_slopes=None,
+                                 q_seqlens=None, kv_rows=None, eps: float = 1e-4,
+                                 tau_iters: int = 120, tol: float = 1e-6):
+    """Selection + decode of one Gaussian-aware step after compute_page_gaussian_moments
+    (ekv_gaussian_paged_entmax_decode): global moments and tau-hat (unless
+    ``tau_hat_given``), threshold select + pack + clamp (``tau_clamped`` None =
+    no clamp), then the given-tau (tau_mode 1) or exact (0) decode."""
+    require_gpu(q, k_cache, v_cache, out, page_indices)
+    B, H, _, D = q.shape
+    Hkv = k_cache.shape[1]
+    if k_cache.stride() != v_cache.stride():
+        raise ValueError("k_cache and v_cache must share strides")
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+        raise TypeError("q, k_cache and v_cache must share a dtype")
+    assert page_indices.dtype == torch.int32 and page_indices.stride(2) == 1
+    assert tuple(page_indices.shape) == (B, Hkv, num_pages), "page_indices shape"
+    max_tokens = num_pages * page_size
+    if workspace.spec[:4] != (B, H, Hkv, D) or workspace.max_tokens < max_tokens:
+        raise ValueError(f"invalid paged workspace {workspace.spec}")
+    auto = safety_margin_z is None or max_quantile is None
+    z_page = page_quantile_z(max_quantile, page_size) if not auto else 0.0
+    smz = float(safety_margin_z) if not auto else 0.0
+    q3 = _row_major_d(q[:, :, 0], "q")
+    o3 = out[:, :, 0]
+    direct = o3.stride(-1) == 1 and o3.data_ptr() % 16 == 0
+    o_target = o3 if direct else torch.empty(B, H, D, device=q.device, dtype=q.dtype)
+    qsl = None if q_seqlens is None else q_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
+    if kv_rows is None:
+        kv_rows = k_cache.shape[2]
+    call("ekv_gaussian_paged_entmax_decode",
+         buffers.ws.data_ptr(), buffers.ws.numel(), buffers.mu_p.data_ptr(),
+         buffers.sigma_p.data_ptr(), pages_for_stats, num_pages, buffers.mu_g.data_ptr(),
+         buffers.sigma_g.data_ptr(), buffers.mean_var.data_ptr(), buffers.var_means.data_ptr(),
+         buffers.tau_hat.data_ptr(), int(bool(tau_hat_given)), int(n_tokens), int(tau_iters),
+         float(tol), int(auto), smz, z_page, page_quantile_z(0.99, page_size),
+         page_quantile_z(0.995, page_size), float(threshold_excess_margin_fraction),
+         page_indices.data_ptr(), page_indices.stride(0), page_indices.stride(1),
+         counts.data_ptr(), tau_floor.data_ptr(), cache_seqlens.data_ptr(), int(last_page_size),
+         ptr(tau_clamped), page_quantile_z(clamp_quantile, page_size), float(eps), ptr(effective),
+         q3.data_ptr(), q3.stride(0), q3.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
+         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), kv_rows, ptr(qsl),
+         ptr(_alibi_f32(alibi_slopes, q.device)), tau_out.data_ptr(), int(tau_mode), int(iters),
+         o_target.data_ptr(), o_target.stride(0), o_target.stride(1), float(alpha),
+         qscale_for(alpha, D, q.dtype), page_size, B, H, Hkv, D, workspace.max_tokens,
+         workspace.buf.data_ptr(), workspace.buf.numel(), dtype_code(q.dtype),
+         stream_ptr(q.device))
+    if not direct:
+        o3.copy_(o_target)
+    return out
+
+
 def solve_for_tau_hat_single_gaussian_gpu(mu_g, sigma_g, n, alpha, iterations=120, tol=1e-6,
                                           out=None):
     """One lane per (b, h) tau-hat; mirrors kernels/tau_solver_gpu.py:128-158."""

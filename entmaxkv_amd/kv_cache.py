@@ -291,6 +291,11 @@ class PagedKVCache:
             counts=sb["counts"], tau_floor=sb["tau_floor"], cache_seqlens=sb["cache_seqlens"],
             last_page_size=last_page_size, tau_clamped=sb["tau_clamped"] if clamp else None,
             clamp_quantile=st.get("tau_clamp_page_max_quantile", 0.5), effective=sb["effective"])
+        self.record_gaussian_selection(st, sb, clamp)
+        return sb["page_indices"], sb["counts"]
+
+    def record_gaussian_selection(self, st: dict, sb: dict, clamp: bool) -> None:
+        """Publish a Gaussian selection's buffers in the stats dict and on the cache."""
         st["tau_floor"] = sb["tau_floor"]
         st["cache_seqlens"] = sb["cache_seqlens"]
         if clamp:
@@ -301,4 +306,3 @@ class PagedKVCache:
         self.last_effective_max_quantile = (
             sb["effective"][1] if st["max_quantile"] is None else st["max_quantile"])
         self.last_num_selected_per_head = sb["counts"]
-        return sb["page_indices"], sb["counts"]

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define EKV_ABI_VERSION 1
+#define EKV_ABI_VERSION 2
 
 const char* ekv_last_error(void);
 int ekv_abi_version(void);
@@ -111,8 +111,22 @@ int ekv_topk_paged_entmax_decode(
     int H, int Hkv, int D, int splits, int max_tokens, void* workspace, int64_t workspace_bytes,
     int dtype, void* stream);
 
-/* Workspace for ekv_gaussian_page_stats. */
+/* Workspace for ekv_gaussian_moments / ekv_gaussian_page_stats (the partial
+ * sums of the global moments; needs no initialisation). */
 int64_t ekv_gaussian_workspace_bytes(int B, int H, int Hkv, int D, int pages, int dtype);
+
+/* Per-page score moments mu_p, sigma_p [B, H, pages_for_stats] (fp32, mu_p
+ * with the ALiBi page-mean bias when alibi_slopes is non-null) and, in the
+ * workspace, each workgroup's partial sums of the global moments: the first
+ * launch of ekv_gaussian_page_stats and of the fused Gaussian step.
+ * Replaces the moment kernel of compute_page_gaussian_stats_triton
+ * (kernels/gaussian_page_stats.py:8-121, 128-233). */
+int ekv_gaussian_moments(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kmean,
+                         const void* kstd, int64_t s_stride_b, int64_t s_stride_h,
+                         int64_t s_stride_page, int pages_for_stats, const float* alibi_slopes,
+                         int page_size, int seq_len, int n_tokens, float* mu_p, float* sigma_p,
+                         int B, int H, int Hkv, int D, void* workspace, int64_t workspace_bytes,
+                         int dtype, void* stream);
 
 /* Per-page score moments mu_p, sigma_p [B, H, pages_for_stats] (fp32; mu_p
  * includes the ALiBi page-mean bias when alibi_slopes is non-null), per-head
@@ -158,6 +172,34 @@ int ekv_select_gaussian_pack(const float* mu_p, const float* sigma_p, const floa
                              float* tau_floor, int32_t* cache_seqlens, int page_size,
                              int last_page_size, float* tau_clamped, float z_clamp, float eps,
                              float* effective_margins, void* stream);
+
+/* One Gaussian-aware decode step after ekv_gaussian_moments (whose workspace
+ * and mu_p / sigma_p it reads): global moments and tau-hat per head (unless
+ * tau_hat_given, e.g. the page-mixture tau-hat under ALiBi), then the
+ * selection of ekv_select_gaussian_pack (tau_clamped null = no clamp), then
+ * the decode of ekv_paged_entmax_decode over the selected pages: tau_mode 1
+ * starts from the clamped tau (or tau-hat) with `iters` corrections, tau_mode
+ * 0 solves tau exactly with `iters` Halley steps.  The page table has
+ * num_pages slots; max_tokens >= num_pages * page_size sizes the decode
+ * workspace.  One launch per step when batch * kv heads fills the GPU,
+ * otherwise the separate launches.  Replaces the selection + decode sequence
+ * of sparse_attention_decode_gaussian_aware_entmax (attention_gaussian.py:
+ * 68-122) with kernels/selection_pack.py:201-272, kernels/tau_clamp.py:76-151
+ * and kernels/adadecode_paged_gaussian_tau.py:192-331. */
+int ekv_gaussian_paged_entmax_decode(
+    const void* moments_workspace, int64_t moments_workspace_bytes, const float* mu_p,
+    const float* sigma_p, int pages_for_stats, int num_pages, float* mu_g, float* sigma_g,
+    float* mean_var, float* var_means, float* tau_hat, int tau_hat_given, int n_tokens,
+    int tau_iters, float tol, int auto_margins, float safety_margin_z, float z_page,
+    float z_page_low, float z_page_high, float threshold_excess_margin_fraction,
+    int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h, int32_t* counts,
+    float* tau_floor, int32_t* cache_seqlens, int last_page_size, float* tau_clamped,
+    float z_clamp, float eps, float* effective_margins, const void* q, int64_t q_stride_b,
+    int64_t q_stride_h, const void* k, const void* v, int64_t kv_stride_b, int64_t kv_stride_h,
+    int64_t kv_stride_row, int64_t kv_rows, const int32_t* q_seqlens, const float* alibi_slopes,
+    float* tau, int tau_mode, int iters, void* out, int64_t out_stride_b, int64_t out_stride_h,
+    float alpha, float qscale, int page_size, int B, int H, int Hkv, int D, int max_tokens,
+    void* workspace, int64_t workspace_bytes, int dtype, void* stream);
 
 /* Standalone tau clamp over a page list (kernels/tau_clamp.py:8-73). */
 int ekv_tau_clamp(const float* tau, const float* mu_p, const float* sigma_p,

@@ -497,3 +497,141 @@ def test_tau_single_matches_oracle():
             torch.cuda.synchronize()
             ref = O.tau_single_gaussian(mu, sg, n, alpha)
             np.testing.assert_allclose(to_np(got), ref, atol=2e-5, rtol=2e-5)
+
+
+def _gqa_gaussian_inputs(rng, dtype, B, Hkv, G, S, D, outlier_frac):
+    """Keys ~ N(mu_h, 1) per kv head with a fraction of pages scaled x3 and pulled
+    toward the group's first query head; q, v ~ N(0, 1)."""
+    H = Hkv * G
+    k = rng.standard_normal((B, Hkv, S, D)) + rng.standard_normal((B, Hkv, 1, 1)) * math.sqrt(0.5)
+    q = rng.standard_normal((B, H, 1, D))
+    P = S // 16
+    n_out = max(1, int(outlier_frac * P))
+    for b in range(B):
+        for kvh in range(Hkv):
+            qh = q[b, kvh * G, 0] / np.linalg.norm(q[b, kvh * G, 0])
+            for p in rng.choice(P, n_out, replace=False):
+                k[b, kvh, p * 16:(p + 1) * 16] = 3.0 * (k[b, kvh, p * 16:(p + 1) * 16] + 4.0 * qh)
+    return O.round_to(q, dtype), O.round_to(k, dtype), randn(rng, (B, Hkv, S, D), dtype)
+
+
+# (dtype, G, tau_mode, alpha); batch * kv heads = 128, so one fused launch per step
+GAUSS_FUSED_CASES = [("fp16", 1, "corrected", 1.5), ("bf16", 1, "exact", 1.5),
+                     ("fp32", 1, "fixed", 2.0), ("fp16", 4, "corrected", 1.5),
+                     ("bf16", 2, "corrected", 2.0), ("fp16", 8, "exact", 1.5)]
+
+
+@pytest.mark.parametrize("dtype,G,tau_mode,alpha", GAUSS_FUSED_CASES)
+def test_gaussian_fused_step(dtype, G, tau_mode, alpha):
+    """The fused Gaussian launch (global moments, tau-hat, selection, clamp and
+    decode in one workgroup per (b, kv head)) against the oracle, stage by stage."""
+    from entmaxkv_amd import PagedKVCache, sparse_attention_decode_gaussian_aware_entmax
+    _case(test="gaussian_fused", dtype=dtype, G=G, tau_mode=tau_mode, alpha=alpha)
+    rng = np.random.default_rng(61 + G)
+    B, Hkv, S, D, ps = 8, 16, 16 * 96 + 5, 64, 16
+    H = Hkv * G
+    q, k, v = _gqa_gaussian_inputs(rng, dtype, B, Hkv, G, S, D, 0.03)
+    cache = PagedKVCache(page_size=ps)
+    cache.initialize(to_dev(k, dtype), to_dev(v, dtype))
+    out = torch.zeros(B, H, 1, D, dtype=TORCH_DT[dtype], device="cuda")
+    sparse_attention_decode_gaussian_aware_entmax(to_dev(q, dtype), cache, None, None, out,
+                                                  alpha=alpha, tau_mode=tau_mode)
+    torch.cuda.synchronize()
+    st = cache.last_gaussian_stats
+    P = cache.num_pages
+    pfs = P - 1
+    lps = O.last_page_size(S, ps)
+    ref = O.gaussian_page_stats(q[:, :, 0], to_np(cache.k_mean), to_np(cache.k_std), pfs)
+    mu_p, sg_p = to_np(st["mu_scores_per_page"]), to_np(st["sigma_scores_per_page"])
+    np.testing.assert_allclose(mu_p, ref["mu_p"], rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(sg_p, ref["sigma_p"], rtol=1e-5, atol=1e-6)
+    mu_g = to_np(st["mu_global"])[..., 0]
+    sg_g = to_np(st["sigma_global"])[..., 0]
+    np.testing.assert_allclose(mu_g, ref["mu_g"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(sg_g, ref["sigma_g"], rtol=1e-5)
+    th = to_np(st["tau_hat"])
+    np.testing.assert_allclose(th, O.tau_single_gaussian(mu_g, sg_g, pfs * ps, alpha),
+                               atol=2e-5, rtol=2e-5)
+    smz, mq = O.auto_selection_margins(sg_g)
+    eff = to_np(st["effective_margins"])
+    np.testing.assert_allclose(eff, [smz, mq], rtol=1e-5)
+    tf = to_np(st["tau_floor"])
+    np.testing.assert_allclose(tf, O.tau_floor_fp32(mu_p, sg_p, th, sg_g, alpha,
+                                                    np.float32(eff[0]), 0.2, pfs),
+                               atol=1e-5, rtol=1e-5)
+    # page table: the union over each kv head's query heads, bit-exact given
+    # the kernel's moments and floor
+    z_page = O.page_quantile_z(0.995 if eff[1] > 0.992 else 0.99, ps)
+    packed_q, _ = O.select_gaussian_pages(mu_p, sg_p, tf, alpha, z_page, pfs, P)
+    counts = to_np(cache.last_num_selected_per_head).astype(np.int64)
+    pidx = to_np(cache._select_buffers[next(iter(cache._select_buffers))]["page_indices"]).astype(np.int64)
+    packed_kv = np.empty((B, Hkv), dtype=object)
+    for b in range(B):
+        for kvh in range(Hkv):
+            u = np.unique(np.concatenate([packed_q[b, kvh * G + g] for g in range(G)]))
+            packed_kv[b, kvh] = u
+            assert counts[b, kvh] == u.size
+            np.testing.assert_array_equal(pidx[b, kvh, :u.size], u)
+            pidx[b, kvh, u.size:] = 0
+    seqlens = O.cache_seqlens_from_counts(counts, ps, lps)
+    np.testing.assert_array_equal(to_np(st["cache_seqlens"]), seqlens)
+    if tau_mode == "exact":
+        ref_out, _ = O.paged_entmax_decode(q[:, :, 0], k, v, pidx, seqlens, ps, alpha, 2, dtype)
+    else:
+        packed_rows = np.empty((B, H), dtype=object)
+        for b in range(B):
+            for h in range(H):
+                packed_rows[b, h] = packed_kv[b, h // G]
+        tc = O.tau_clamp(th, mu_p, sg_p, packed_rows, np.repeat(counts, G, axis=1), tf, alpha,
+                         O.page_quantile_z(0.5, ps), pfs)
+        np.testing.assert_allclose(to_np(st["tau_clamped"]), tc, atol=1e-6, rtol=1e-6)
+        iters = 0 if tau_mode == "fixed" else 1
+        tau_in = to_np(st["tau_clamped"])
+        tau_fin = to_np(st["tau_final"])
+        ref_out, ref_tau = O.paged_entmax_decode(q[:, :, 0], k, v, pidx, seqlens, ps, alpha, 0,
+                                                 dtype, tau_given=tau_in, tau_iters=iters)
+        # The corrected tau: for alpha = 1.5 the Halley step's second-derivative term
+        # counts the support, which jumps by one when a score ties tau_in within fp32
+        # rounding; rows with such a near-tie are compared through the sum only.
+        qs = O.scaled_query(q[:, :, 0], alpha, dtype)
+        mass = np.ones((B, H, 1))
+        tie = np.zeros((B, H), dtype=bool)
+        cond = np.ones((B, H))
+        for b in range(B):
+            for h in range(H):
+                rows = O.compacted_rows(pidx[b, h // G], seqlens[b, h // G], ps)
+                sc = O.head_scores(qs[b, h], k[b, h // G], rows, 0.0, alpha, 0)
+                tie[b, h] = iters > 0 and bool(
+                    (np.abs(sc - tau_in[b, h]) < 1e-5 * max(1.0, np.abs(sc).max())).any())
+                mass[b, h, 0] = max(1.0, O.entmax_weights(sc, ref_tau[b, h], alpha).sum())
+                if iters:
+                    # condition of the unbounded Halley step (adadecode_paged_gaussian_tau.py:
+                    # 12-53): 2 f'^2 - f f'' can nearly cancel, and the step then amplifies
+                    # the fp32 rounding of the accumulators by (2 f'^2 + |f f''|) / |denominator|
+                    a0, a1, a2 = O.entmax_accumulators(sc, tau_in[b, h], alpha)
+                    c0 = 1.0 / (alpha - 1.0)
+                    f, df, ddf = a0 - 1.0, -c0 * a1, c0 * (c0 - 1.0) * a2
+                    den = abs(2 * df * df - f * ddf)
+                    cond[b, h] = (2 * df * df + abs(f * ddf)) / den if den > 0 else np.inf
+        assert tie.mean() < 0.05, f"{tie.sum()} near-tie rows"
+        with np.errstate(invalid="ignore"):
+            amp = np.nan_to_num(np.abs(ref_tau - tau_in) * cond, nan=0.0)
+        tol = 1e-4 + 1e-5 * np.abs(ref_tau) + 1e-5 * amp
+        bad = (np.abs(tau_fin - ref_tau) > tol) & ~tie
+        assert not bad.any(), (f"tau_final: {bad.sum()} rows beyond tolerance, worst "
+                               f"{np.abs(tau_fin - ref_tau)[bad].max():.3g}")
+        # the weighted sum at the kernel's own final tau
+        ref_at_fin, _ = O.paged_entmax_decode(q[:, :, 0], k, v, pidx, seqlens, ps, alpha, 0,
+                                              dtype, tau_given=tau_fin, tau_iters=0)
+        # given tau, out = sum_i [s_i - tau]_+^(1/(alpha-1)) v_i is not normalised: its
+        # weights sum to `mass`, not 1, so the bar scales with max(1, mass)
+        got = to_np(out)[:, :, 0]
+        # an un-normalised sum beyond the storage range is stored as +-inf
+        big = np.abs(ref_at_fin) > {"fp16": 65504.0, "bf16": 3.3e38, "fp32": 3.4e38}[dtype]
+        assert (np.isinf(got[big]) & (np.sign(got[big]) == np.sign(ref_at_fin[big]))).all()
+        got = np.where(big, 0.0, got)
+        assert_out_close(got / mass, np.where(big, 0.0, ref_at_fin) / mass, dtype)
+        ok = ~tie[..., None] & ~big
+        assert_out_close((got / mass)[ok], (ref_out / mass)[ok], dtype)
+        return
+    assert_out_close(to_np(out)[:, :, 0], ref_out, dtype)
