@@ -24,6 +24,19 @@
 // kernels and reads K 3 + niter times.
 #pragma once
 
+// Experiment builds only (-DEKV_PHASE_TIMERS on one decode_inst unit):
+// per-workgroup wall-clock stamps (100 MHz) of the fused kernels' phases.
+#ifdef EKV_PHASE_TIMERS
+__device__ unsigned long long ekv_phase_timers[4096 * 8];
+#define EKV_STAMP(i) \
+  if (threadIdx.x == 0 && blockIdx.x < 4096) ekv_phase_timers[blockIdx.x * 8 + (i)] = wall_clock64()
+// slot 6 in the top-k launch: the top-k threshold found (topk_device.h stamp 3)
+#define EKV_CSTAMP(i) \
+  if ((i) == 3) EKV_STAMP(6)
+#else
+#define EKV_STAMP(i)
+#endif
+
 #include "ekv_common.h"
 #include "topk_device.h"
 #include "gaussian_device.h"
@@ -143,9 +156,10 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
   }
   const T* kh = (const T*)a.k + b * a.ksb + kvh * a.ksh;
   const int ps = a.page_size;
-  for (int c0 = c_begin; c0 < c_end; c0 += ROWS) {
-    uint4 kv[U];
-    int rows[U];  // row within the (b, kv head); the cache holds < 2^31 rows per head
+  // Rows of compacted tokens c0 + u * SEGS + seg and their K loads.  The loads
+  // are unconditional (an invalid token re-reads row 0 and is masked), so
+  // all U of them are in flight together.
+  auto fetch = [&](int c0, int (&rows)[U], uint4 (&kv)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = c0 + u * SEGS + seg;
@@ -157,14 +171,15 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (rows[u] >= 0) kv[u] = ld16(kh + (int64_t)rows[u] * a.ksr + col);
+    for (int u = 0; u < U; ++u) kv[u] = ld16(kh + (int64_t)max(rows[u], 0) * a.ksr + col);
+  };
+  auto consume = [&](int c0, const int (&rows)[U], const uint4 (&kv)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = c0 + u * SEGS + seg;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float acc = rows[u] >= 0 ? Dot16<T>::dot(qraw[g], kv[u], 0.f) : 0.f;
+        float acc = Dot16<T>::dot(qraw[g], kv[u], 0.f);
         acc = seg_sum<LPR>(acc);
         if (c < c_end && sl == 0) {
           float s = acc;
@@ -174,6 +189,18 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
         }
       }
     }
+  };
+  // two register buffers: the loads of the next round are issued before the
+  // current round's arithmetic
+  int rows_a[U], rows_b[U];
+  uint4 kv_a[U], kv_b[U];
+  if (c_begin < c_end) fetch(c_begin, rows_a, kv_a);
+  for (int c0 = c_begin; c0 < c_end; c0 += 2 * ROWS) {
+    if (c0 + ROWS < c_end) fetch(c0 + ROWS, rows_b, kv_b);
+    consume(c0, rows_a, kv_a);
+    if (c0 + ROWS >= c_end) break;
+    if (c0 + 2 * ROWS < c_end) fetch(c0 + 2 * ROWS, rows_a, kv_a);
+    consume(c0 + ROWS, rows_b, kv_b);
   }
 }
 
@@ -508,7 +535,8 @@ __device__ __forceinline__ void solve_heads(const DecodeArgs& a, int b, int h0, 
 // score access is a ds_* instruction) and to the workspace otherwise.
 template <typename T, int LPR, int G, int U, bool kStaged, bool kTableInLds = false>
 __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int kvh, int n,
-                                                 float* sc, int64_t stride, const HeadShared& sh) {
+                                                 float* sc, int64_t stride, const HeadShared& sh,
+                                                 bool first_chunk_staged = false) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int SEGS = kHeadThreads / LPR;
   constexpr int D = LPR * VEC;
@@ -526,13 +554,16 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
     for (int cb = 0; cb < n; cb += kTablePages * ps) {
       const int ce = min(n, cb + kTablePages * ps);
       const int np = (ce - cb + ps - 1) / ps;
-      for (int i = tid; i < np; i += kHeadThreads) sh.s_pages[i] = pi[cb / ps + i];
+      if (!(first_chunk_staged && cb == 0)) {
+        for (int i = tid; i < np; i += kHeadThreads) sh.s_pages[i] = pi[cb / ps + i];
+      }
       __syncthreads();
       score_rows<T, LPR, G, kHeadThreads, U>(a, b, kvh, cb, ce, sc, stride, sh.s_pages, cb);
       __syncthreads();
     }
   }
   __syncthreads();
+  EKV_STAMP(3);
 
   // phase 2: tau per head, one team of waves per head
   if (n <= kWaveTauMax) {
@@ -545,6 +576,7 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
 #pragma unroll
   for (int g = 0; g < G; ++g) tau[g] = sh.s_tau[g];
   if (tid < G) a.tau[b * a.H + h0 + tid] = sh.s_tau[tid];
+  EKV_STAMP(4);
 
   // phase 3: gather the support's V rows
   const float alpha = a.alpha;
@@ -596,25 +628,28 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
       for (int g = 0; g < G; ++g) sh.sup_p[g * kHeadThreads + slot] = p[g];
     }
     __syncthreads();
-    for (int j0 = seg; j0 < nsup; j0 += 2 * SEGS) {
-      const int j1 = j0 + SEGS;
-      Vec<T> x0, x1;
-      x0.load(vh + sh.sup_row[j0] * a.ksr + col);
-      if (j1 < nsup) x1.load(vh + sh.sup_row[j1] * a.ksr + col);
+    // four support rows per segment in flight (a slot past nsup re-reads the
+    // last row and is not accumulated)
+    for (int j0 = seg; j0 < nsup; j0 += 4 * SEGS) {
+      Vec<T> x[4];
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float w0 = sh.sup_p[g * kHeadThreads + j0];
+      for (int r = 0; r < 4; ++r) x[r].load(vh + sh.sup_row[min(j0 + r * SEGS, nsup - 1)] * a.ksr + col);
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[g][i] += w0 * x0.v[i];
-        if (j1 < nsup) {
-          const float w1 = sh.sup_p[g * kHeadThreads + j1];
+      for (int r = 0; r < 4; ++r) {
+        const int j = j0 + r * SEGS;
+        if (j < nsup) {
 #pragma unroll
-          for (int i = 0; i < VEC; ++i) acc[g][i] += w1 * x1.v[i];
+          for (int g = 0; g < G; ++g) {
+            const float w = sh.sup_p[g * kHeadThreads + j];
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) acc[g][i] += w * x[r].v[i];
+          }
         }
       }
     }
     __syncthreads();
   }
+  EKV_STAMP(5);
 
   // reduce the row segments: within each wave by shuffles, then across waves
 #pragma unroll
@@ -701,15 +736,18 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
   const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
   uint32_t* keys = reinterpret_cast<uint32_t*>(stage);
   const bool keep = t.num_pages <= t.key_cap;
+  EKV_STAMP(0);
   const T* sbase = topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC>(
       (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
       a.slopes, (T*)t.scores, a.H, t.num_pages, a.page_size, t.seq_len, t.q_pos, b, kvh,
       keep ? keys : nullptr);
   __syncthreads();
+  EKV_STAMP(1);
   int32_t* pi = const_cast<int32_t*>(a.page_indices) + b * a.pisb + kvh * a.pish;
   topk::topk_select_block<T, G, kHeadThreads>(sbase, t.num_pages, t.num_pages, t.k, t.last_page,
                                               pi, keys, keep ? t.num_pages : 0, keep, s_pages);
   __syncthreads();
+  EKV_STAMP(2);
   const int n = token_count(a, b, kvh);
   decode_head_body<T, LPR, G, UD, true, true>(a, b, kvh, n, stage, a.stage_cap, sh);
 }
@@ -751,7 +789,7 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
   __shared__ float red[kWaves * D];
   __shared__ int s_pages[kTablePages];
   __shared__ float s_th[G], s_sg[G], s_tin[G];
-  __shared__ float scratch[16];
+  __shared__ float scratch[kWaves];
   HeadShared sh{hist, part, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
   sh.tau_in_lds = s_tin;
 
@@ -759,24 +797,32 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
   const int bkv = blockIdx.x;
   const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
   const gauss::SelectArgs& sel = f.sel;
-  float sbar = 0.f;
-  if (sel.auto_margins) {
-    float s = 0.f;
-    const int nh = sel.B * sel.H;
-    for (int i = tid; i < nh; i += kHeadThreads)
-      s += gauss::finalize_moments(gauss::head_sums(f.partials, i, f.splits), sel.pages).sigma_g;
-    sbar = block_sum(s, scratch) / (float)nh;
-  }
+  EKV_STAMP(0);
+  // Global moments from the moments launch's partials, reduced over aligned
+  // groups of S2 lanes (one fixed lane-tree, so every consumer derives the same
+  // bits).  Wave g < G reduces its own head and solves its tau-hat while the
+  // other waves reduce every head of the batch for the mean sigma_g of the
+  // automatic margins.
+  const int nh = sel.B * sel.H;
+  const int s2 = gauss::split_lanes(f.splits);
+  const int own0 = b * a.H + kvh * G;
+  const int lane = tid & 63;
   if (wid < G) {
-    const int h = b * a.H + kvh * G + wid;
-    const gauss::Moments m =
-        gauss::finalize_moments(gauss::head_sums(f.partials, h, f.splits), sel.pages);
+    const int h = own0 + wid;
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (lane < f.splits) x = f.partials[(int64_t)h * f.splits + lane];
+    if (lane >= s2) x = make_float4(0.f, 0.f, 0.f, 0.f);
+    x = gauss::reduce_splits(x, s2);
+    x.x = __shfl(x.x, 0);
+    x.y = __shfl(x.y, 0);
+    x.z = __shfl(x.z, 0);
+    const gauss::Moments m = gauss::finalize_moments(x, sel.pages);
     const float th = f.tau_hat_given
                          ? f.tau_hat[h]
                          : gauss::solve_single_gaussian_wave(m.mu_g, m.sigma_g, f.n_tokens,
                                                              f.tau_alpha, f.log_n_factor,
                                                              f.tau_iters, f.tol);
-    if ((tid & 63) == 0) {
+    if (lane == 0) {
       s_th[wid] = th;
       s_sg[wid] = m.sigma_g;
       f.mu_g[h] = m.mu_g;
@@ -785,20 +831,44 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
       f.var_means[h] = m.var_means;
       if (!f.tau_hat_given) f.tau_hat[h] = th;
     }
+  } else if (sel.auto_margins) {
+    const int nt = (kWaves - G) * 64, t = tid - G * 64;
+    const int hpp = nt / s2;  // heads per pass
+    float ssum = 0.f;
+    for (int base = 0; base < nh; base += hpp) {
+      const int h = base + t / s2, j = t % s2;
+      const bool ok = t < hpp * s2 && h < nh;
+      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (ok && j < f.splits) x = f.partials[(int64_t)h * f.splits + j];
+      x = gauss::reduce_splits(x, s2);
+      if (ok && j == 0) ssum += gauss::finalize_moments(x, sel.pages).sigma_g;
+    }
+    ssum = wave_sum(ssum);
+    if (lane == 0) scratch[wid] = ssum;
   }
   __syncthreads();
-  const int count =
-      gauss::select_pack_block<G, kHeadThreads>(sel, b, kvh, sbar, s_th, s_sg, nullptr, 0, s_tin);
+  float sbar = 0.f;
+  if (sel.auto_margins) {
+    for (int w = G; w < kWaves; ++w) sbar += scratch[w];
+    sbar /= (float)nh;
+  }
+  EKV_STAMP(6);
+  EKV_STAMP(1);
+  const int count = gauss::select_pack_block<G, kHeadThreads>(sel, b, kvh, sbar, s_th, s_sg,
+                                                              s_pages, kTablePages, s_tin);
   __syncthreads();
+  EKV_STAMP(2);
+
   // compacted length max(count - 1, 0) * ps + last_page_size; an empty table
   // attends to nothing
   int n = count > 0 ? (count - 1) * sel.page_size + sel.last_page_size : 0;
   n = min(n, min(count * sel.page_size, a.max_tokens));
+  // the first kTablePages page ids are already in s_pages
   if (n <= a.stage_cap) {
-    decode_head_body<T, LPR, G, UD, true>(a, b, kvh, n, stage, a.stage_cap, sh);
+    decode_head_body<T, LPR, G, UD, true>(a, b, kvh, n, stage, a.stage_cap, sh, true);
   } else {
     float* ws = a.ws_scores + ((int64_t)b * a.H + kvh * G) * a.max_tokens;
-    decode_head_body<T, LPR, G, UD, false>(a, b, kvh, n, ws, a.max_tokens, sh);
+    decode_head_body<T, LPR, G, UD, false>(a, b, kvh, n, ws, a.max_tokens, sh, true);
   }
 }
 

@@ -14,3 +14,10 @@ template struct ekv::dec::Launch<_Float16, EKV_INST_G>;
 #else
 template struct ekv::dec::Launch<ekv::bf16_t, EKV_INST_G>;
 #endif
+
+#ifdef EKV_PHASE_TIMERS
+extern "C" int ekv_debug_phase_timers(unsigned long long* host, int n) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(ekv_phase_timers),
+                                  n * sizeof(unsigned long long));
+}
+#endif

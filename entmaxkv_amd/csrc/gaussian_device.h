@@ -125,11 +125,13 @@ __device__ __forceinline__ float solve_single_gaussian(float mu, float sigma, fl
   return t;
 }
 
-// The same root solved by a whole wave (every lane returns it): three rounds
-// of a 64-point bracket search (f is decreasing in tau, so the positive lanes
-// form a prefix; the bracket shrinks 65x per round), then bracketed Halley
-// steps from the middle of the final bracket.  Ten function evaluations
-// instead of up to 2 * iterations on one lane.
+// The same root solved by a whole wave (every lane returns it): two rounds of
+// a 64-point bracket search (f is decreasing in tau, so the positive lanes
+// form a prefix; the bracket shrinks 65x per round), then Halley steps with
+// bisection fallback from the middle of the final bracket, one evaluation of
+// f per step, until |f(t)| <= tol and the next step is below
+// 1e-6 * max(1, |t|) (at most `iterations`, capped at 8).  About five
+// function evaluations in all.
 __device__ __forceinline__ float solve_single_gaussian_wave(float mu, float sigma, float n,
                                                             float alpha, float log_n_factor,
                                                             int iterations, float tol) {
@@ -139,7 +141,7 @@ __device__ __forceinline__ float solve_single_gaussian_wave(float mu, float sigm
   float lo = a * mu - radius, hi = a * mu + radius;
   const int lane = threadIdx.x & 63;
 #pragma unroll 1
-  for (int r = 0; r < 3; ++r) {
+  for (int r = 0; r < 2; ++r) {
     const float w = (hi - lo) * (1.0f / 65.0f);
     const float x = fmaf(w, (float)(lane + 1), lo);
     float e, d1, d2;
@@ -153,9 +155,27 @@ __device__ __forceinline__ float solve_single_gaussian_wave(float mu, float sigm
     hi = fmaxf(nhi, nlo);
   }
   float t = 0.5f * (lo + hi);
-  const int steps = iterations < 4 ? iterations : 4;
-  for (int it = 0; it < steps; ++it)
-    if (halley_bracket_step(t, lo, hi, mu, sigma, n, alpha, tol)) break;
+  const int steps = iterations < 8 ? iterations : 8;
+  for (int it = 0; it < steps; ++it) {
+    float e, f1, f2;
+    gaussian_terms(t, mu, sigma, n, alpha, e, f1, f2);
+    const float f = e - 1.0f;
+    if (f > 0.0f) lo = t;
+    else hi = t;
+    const float den = 2.0f * f1 * f1 - f * f2;
+    const float step = fabsf(den) > 1.0e-18f ? 2.0f * f * f1 / den : f / fminf(f1, -1.0e-12f);
+    // converged at t: the test comes before the bracket check, since a step
+    // this small can round onto the bracket edge
+    // or stalled: a step or a bracket of a few ulps is fp32 noise in f
+    // (the reference's moment formulas cancel), not progress
+    const float scale_t = fmaxf(1.0f, fabsf(t));
+    if ((fabsf(f) <= tol && fabsf(step) <= 1.0e-6f * scale_t) || fabsf(step) <= 2.4e-7f * scale_t ||
+        hi - lo <= 4.8e-7f * scale_t)
+      break;
+    float cand = t - step;
+    if (!(cand == cand && fabsf(cand) < 1.0e20f && cand > lo && cand < hi)) cand = 0.5f * (lo + hi);
+    t = cand;
+  }
   return t;
 }
 
@@ -222,15 +242,16 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
   for (int g = 0; g < G; ++g) s_mu[g] = s_mu2[g] = s_var[g] = 0.f;
 
   for (int p0 = p_begin; p0 < p_end; p0 += SEGS * U) {
+    // unconditional loads (a page past the end re-reads the last one, its
+    // result is discarded) so that all 2U loads are in flight together
     VecRaw<T> mv[U], sv[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int p = p0 + u * SEGS + seg;
-      if (p < p_end) {
-        mv[u].load(km + (int64_t)p * a.ssp + col);
-        sv[u].load(ks + (int64_t)p * a.ssp + col);
-      }
+      const int p = min(p0 + u * SEGS + seg, p_end - 1);
+      mv[u].load(km + (int64_t)p * a.ssp + col);
+      sv[u].load(ks + (int64_t)p * a.ssp + col);
     }
+    __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the arithmetic
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int p = p0 + u * SEGS + seg;
@@ -238,13 +259,11 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float mu = 0.f, var = 0.f;
-        if (ok) {
 #pragma unroll
-          for (int i = 0; i < VEC; ++i) {
-            const float sd = sv[u].get(i);
-            mu += mv[u].get(i) * qs[g][i];
-            var += (sd * sd) * qq[g][i];
-          }
+        for (int i = 0; i < VEC; ++i) {
+          const float sd = sv[u].get(i);
+          mu += mv[u].get(i) * qs[g][i];
+          var += (sd * sd) * qq[g][i];
         }
         mu = seg_sum<LPR>(mu);
         var = seg_sum<LPR>(var);
@@ -286,18 +305,32 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
   }
 }
 
-// Sum of one head's partials, in split order.
-__device__ __forceinline__ float4 head_sums(const float4* __restrict__ partials, int64_t head,
-                                            int splits) {
-  const float4* p = partials + head * splits;
-  float4 r = p[0];
-  for (int s = 1; s < splits; ++s) {
-    const float4 y = p[s];
-    r.x += y.x;
-    r.y += y.y;
-    r.z += y.z;
+// Sum of one head's `splits` partials held by an aligned segment of
+// S2 = split_lanes(splits) lanes (lane j of the segment holds partial j, the
+// lanes past `splits` hold zeros); every lane of the segment receives the
+// sum.  The lane-tree order is fixed, so every consumer of a head's partials
+// (the standalone finalize launch and the fused step) derives the same bits.
+__host__ __device__ __forceinline__ int split_lanes(int splits) {
+  int s2 = 1;
+  while (s2 < splits) s2 *= 2;
+  return s2;
+}
+
+template <int L>
+__device__ __forceinline__ float4 seg_sum4(float4 x) {
+  return make_float4(seg_sum<L>(x.x), seg_sum<L>(x.y), seg_sum<L>(x.z), 0.f);
+}
+
+__device__ __forceinline__ float4 reduce_splits(float4 x, int s2) {
+  switch (s2) {
+    case 1: return x;
+    case 2: return seg_sum4<2>(x);
+    case 4: return seg_sum4<4>(x);
+    case 8: return seg_sum4<8>(x);
+    case 16: return seg_sum4<16>(x);
+    case 32: return seg_sum4<32>(x);
+    default: return seg_sum4<64>(x);
   }
-  return r;
 }
 
 struct Moments {

@@ -38,8 +38,8 @@ __global__ __launch_bounds__(kThreads) void moments_kernel(MomentsArgs a) {
                                                             blockIdx.x);
 }
 
-// One wave per (b, h): global moments from the partials and (optional) the
-// single-Gaussian tau-hat.
+// One wave per (b, h): global moments from the partials (reduced by the
+// first split_lanes(splits) lanes) and (optional) the single-Gaussian tau-hat.
 __global__ __launch_bounds__(kThreads) void finalize_kernel(const float4* partials, int splits,
                                                             int pages, int count, float* mu_g,
                                                             float* sigma_g, float* mean_var,
@@ -49,11 +49,20 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const float4* partia
                                                             float tol) {
   const int head = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
   if (head >= count) return;
-  const Moments m = finalize_moments(head_sums(partials, head, splits), pages);
+  const int lane = threadIdx.x & 63;
+  const int s2 = split_lanes(splits);
+  float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (lane < splits) x = partials[(int64_t)head * splits + lane];
+  if (lane >= s2) x = make_float4(0.f, 0.f, 0.f, 0.f);
+  x = reduce_splits(x, s2);
+  x.x = __shfl(x.x, 0);
+  x.y = __shfl(x.y, 0);
+  x.z = __shfl(x.z, 0);
+  const Moments m = finalize_moments(x, pages);
   float th = 0.f;
   if (tau_hat)
     th = solve_single_gaussian_wave(m.mu_g, m.sigma_g, n_tokens, alpha, log_n_factor, iters, tol);
-  if ((threadIdx.x & 63) == 0) {
+  if (lane == 0) {
     mu_g[head] = m.mu_g;
     sigma_g[head] = m.sigma_g;
     mean_var[head] = m.mean_var;

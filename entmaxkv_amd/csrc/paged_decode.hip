@@ -88,7 +88,7 @@ extern "C" int ekv_paged_entmax_decode(
   EKV_REQUIRE(q && k && v && page_indices && cache_seqlens && tau && out && workspace,
               "ekv_paged_entmax_decode: null pointer");
   EKV_REQUIRE(B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0, "ekv_paged_entmax_decode: bad heads");
-  EKV_REQUIRE(page_size > 0 && n_slots > 0 && splits > 0 && max_tokens > 0,
+  EKV_REQUIRE(page_size > 0 && n_slots > 0 && splits > 0 && max_tokens > 0 && kv_rows > 0,
               "ekv_paged_entmax_decode: bad sizes");
   EKV_REQUIRE(tau_mode == 0 || tau_mode == 1, "ekv_paged_entmax_decode: tau_mode %d", tau_mode);
   EKV_REQUIRE(tau_mode == 0 || tau_in, "ekv_paged_entmax_decode: given-tau mode needs tau_in");
@@ -134,7 +134,7 @@ extern "C" int ekv_topk_paged_entmax_decode(
   EKV_REQUIRE(num_pages > 0 && k_select > 0 && k_select <= num_pages && page_size > 0,
               "ekv_topk_paged_entmax_decode: bad page selection (k %d of %d pages)", k_select,
               num_pages);
-  EKV_REQUIRE(niter >= 0 && alpha > 1.0f && splits > 0 && max_tokens > 0,
+  EKV_REQUIRE(niter >= 0 && alpha > 1.0f && splits > 0 && max_tokens > 0 && kv_rows > 0,
               "ekv_topk_paged_entmax_decode: bad decode parameters");
   EKV_REQUIRE(workspace_bytes >= ekv_decode_workspace_bytes(B, H, Hkv, D, splits, max_tokens),
               "ekv_topk_paged_entmax_decode: workspace too small");
@@ -220,7 +220,7 @@ extern "C" int ekv_gaussian_paged_entmax_decode(
               "ekv_gaussian_paged_entmax_decode: tau-hat needs alpha in {2, 1.5, 4/3}");
   EKV_REQUIRE(tau_mode == 0 || tau_mode == 1, "ekv_gaussian_paged_entmax_decode: tau_mode %d",
               tau_mode);
-  EKV_REQUIRE(iters >= 0 && max_tokens >= num_pages * page_size,
+  EKV_REQUIRE(iters >= 0 && max_tokens >= num_pages * page_size && kv_rows > 0,
               "ekv_gaussian_paged_entmax_decode: bad decode parameters");
   EKV_REQUIRE(workspace_bytes >= ekv_decode_workspace_bytes(B, H, Hkv, D, 1, max_tokens),
               "ekv_gaussian_paged_entmax_decode: workspace too small");
