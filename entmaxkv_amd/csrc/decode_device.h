@@ -817,6 +817,7 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
     x.y = __shfl(x.y, 0);
     x.z = __shfl(x.z, 0);
     const gauss::Moments m = gauss::finalize_moments(x, sel.pages);
+    EKV_STAMP(7);
     const float th = f.tau_hat_given
                          ? f.tau_hat[h]
                          : gauss::solve_single_gaussian_wave(m.mu_g, m.sigma_g, f.n_tokens,
