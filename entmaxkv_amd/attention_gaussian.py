@@ -41,6 +41,8 @@ def sparse_attention_decode_gaussian_aware_entmax(
     ``tau_correction_iters`` (default 1, 2 with ALiBi) Halley corrections.
     As in the reference, ``safety_margin_z`` and ``max_quantile`` are superseded
     by the automatic margins and ``scale`` is unused (the kernel uses 1/sqrt(D)).
+    A ragged cache (``kv_cache.seq_lens``) gives every sequence its own pages,
+    statistics and tau-hat; the automatic margins stay batch-wide.
     Launches: [append] -> page moments -> [page-mixture tau-hat under ALiBi]
     -> one launch of global moments + tau-hat + select + pack + clamp +
     decode (separate launches when batch * kv heads is too small to fill the
@@ -71,14 +73,19 @@ def sparse_attention_decode_gaussian_aware_entmax(
     if alpha not in (2, 1.5, 4 / 3):
         raise ValueError(f"Unsupported alpha for the Gaussian tau solve: {alpha}")
     buf = kv_cache.get_gaussian_buffers(q, pages_for_stats)
+    seq_lens = kv_cache.seq_lens
+    if q_seqlens is None and seq_lens is not None:
+        q_seqlens = seq_lens
     K.compute_page_gaussian_moments(q, kv_cache.k_mean, kv_cache.k_std, pages_for_stats, buf,
                                     alibi_slopes=alibi_slopes, page_size=page_size,
-                                    seq_len=seq_len, n_tokens=seq_len_for_stats)
+                                    seq_len=seq_len, n_tokens=seq_len_for_stats,
+                                    seq_lens=seq_lens)
     tau_hat_given = alibi_slopes is not None
     if tau_hat_given:
         # ALiBi: page-mixture tau-hat over the biased page means (gaussian_utils.py:171-181)
         tau_mix = solve_for_tau_hat_page_gaussian_mixture_auto(
-            buf.mu_p, buf.sigma_p, alpha=alpha, uniform_page_count=float(page_size))
+            buf.mu_p, buf.sigma_p, alpha=alpha, uniform_page_count=float(page_size),
+            seq_lens=seq_lens, page_size=page_size)
         buf.tau_hat.copy_(tau_mix.squeeze(-1))
     gaussian_stats = stats_dict(buf, seq_len_for_stats, pages_for_stats, num_pages,
                                 threshold_excess_margin_fraction, tau_clamp_page_max_quantile)
@@ -111,7 +118,8 @@ def sparse_attention_decode_gaussian_aware_entmax(
         tau_clamped=sb["tau_clamped"] if do_clamp else None,
         clamp_quantile=tau_clamp_page_max_quantile, effective=sb["effective"],
         tau_out=workspace.taus, tau_mode=dec_mode, iters=iters, workspace=workspace,
-        alibi_slopes=alibi_slopes, q_seqlens=q_seqlens, kv_rows=kv_cache.kv_capacity)
+        alibi_slopes=alibi_slopes, q_seqlens=q_seqlens, kv_rows=kv_cache.kv_capacity,
+        seq_lens=seq_lens)
     kv_cache.record_gaussian_selection(gaussian_stats, sb, do_clamp)
     if tau_mode != "exact":
         gaussian_stats["tau_final"] = workspace.taus

@@ -33,6 +33,10 @@ def sparse_attention_decode_paged(
     caller, as in the reference (n_selected * page_size + last_page_size).
     ``splits`` and ``use_triton_criticality`` are accepted for compatibility.
     Under GQA the page table is per kv head (group maximum of page scores).
+    Ragged cache (``kv_cache.seq_lens``): each sequence selects
+    min(budget // ps, P_b - 1) pages of its own; ``cache_seqlens`` may then be
+    None (derived per sequence, ``PagedKVCache.compacted_seqlens``) and
+    ``q_seqlens`` defaults to the sequence lengths.
     """
     batch, num_heads, _, head_dim = q.shape
     num_kv_heads = kv_cache.k_cache.shape[1]
@@ -42,6 +46,11 @@ def sparse_attention_decode_paged(
 
     seq_len = kv_cache.seq_len
     page_size = kv_cache.page_size
+    seq_lens = kv_cache.seq_lens
+    if cache_seqlens is None:
+        cache_seqlens = kv_cache.compacted_seqlens(token_budget)
+    if q_seqlens is None and seq_lens is not None:
+        q_seqlens = seq_lens
     total_pages = (seq_len + page_size - 1) // page_size
     num_pages_to_select = min(token_budget // page_size, total_pages - 1)
 
@@ -67,5 +76,5 @@ def sparse_attention_decode_paged(
         q, kv_cache.k_min, kv_cache.k_max, scores, num_pages_to_select, last, kv_cache._k,
         kv_cache._v, out, page_indices, cache_seqlens, page_size, alpha, niter, seq_len,
         seq_len - 1, alibi_slopes=alibi_slopes, q_seqlens=q_seqlens, workspace=workspace,
-        kv_rows=kv_cache.kv_capacity)
+        kv_rows=kv_cache.kv_capacity, seq_lens=seq_lens)
     return out

@@ -9,12 +9,17 @@
 //   sentinel.  Replaces torch.topk + the index buffer of attention_topk.py:52-71
 //   and kv_cache.py:167-185.
 //
-// Layout: one workgroup (256 threads) scores PAGES_PER_WG pages of one
-// (b, kv head); a row segment of LPR lanes owns one page and loads its kmin
-// and kmax rows with 16-byte loads.  Every page is read once for all G query
-// heads of the group.  When top-k is fused, the last workgroup of a
-// (b, kv head) to finish runs a block-wide radix select over the page scores
-// (already resident in L2) and writes the page table.
+// Ragged batches (seq_lens non-null): every (b, kv head) scores, selects and
+// appends the sentinel for its own length (ragged_topk, topk_device.h);
+// `num_pages` is then the score row stride (the longest sequence).
+//
+// Layout: with B * Hkv >= 128, one workgroup per (b, kv head) scores every
+// page of the head and selects its top-k in the same launch
+// (criticality_head_kernel); otherwise each head's pages are spread over
+// workgroups of 256 threads (criticality_kernel) and a second launch selects
+// (topk_kernel).  A row segment of LPR lanes owns one page and loads its kmin
+// and kmax rows with 16-byte loads; every page is read once for all G query
+// heads of the group.
 #include "ekv_common.h"
 
 #ifdef EKV_PHASE_TIMERS
@@ -46,31 +51,33 @@ template <typename T, int LPR, int G, int U>
 __global__ __launch_bounds__(kHeadThreads) void criticality_head_kernel(
     const T* __restrict__ q, int64_t qsb, int64_t qsh, const T* __restrict__ kmin,
     const T* __restrict__ kmax, int64_t ssb, int64_t ssh, int64_t ssp,
-    const float* __restrict__ slopes, T* __restrict__ scores, int H, int Hkv, int num_pages,
-    int page_size, int seq_len, int q_pos, int k_sel, int last_page, int32_t* page_indices,
-    int64_t pisb, int64_t pish, int lds_key_cap) {
+    const float* __restrict__ slopes, T* __restrict__ scores, int H, int Hkv, int stride,
+    int page_size, int seq_len, int q_pos, int k_sel, int last_page,
+    const int32_t* __restrict__ seq_lens, int32_t* page_indices, int64_t pisb, int64_t pish,
+    int lds_key_cap) {
   extern __shared__ uint32_t lds_keys[];
   const int bkv = blockIdx.x;
   const int b = bkv / Hkv, kvh = bkv % Hkv;
-  const bool keep_keys = k_sel >= 0 && num_pages <= lds_key_cap;
+  const Ragged r = ragged_topk(seq_lens, b, page_size, stride, seq_len, q_pos, k_sel, last_page);
+  const bool keep_keys = r.k >= 0 && r.count <= lds_key_cap;
   EKV_CSTAMP(0);
   T* sbase = criticality_scan_head<T, LPR, G, kHeadThreads, U>(
-      q, qsb, qsh, kmin, kmax, ssb, ssh, ssp, slopes, scores, H, num_pages, page_size, seq_len,
-      q_pos, b, kvh, keep_keys ? lds_keys : nullptr);
-  if (k_sel < 0) return;
+      q, qsb, qsh, kmin, kmax, ssb, ssh, ssp, slopes, scores, H, stride, r.count, page_size,
+      r.seq_len, r.q_pos, b, kvh, keep_keys ? lds_keys : nullptr);
+  if (r.k < 0) return;
   __syncthreads();
   EKV_CSTAMP(1);
-  topk_select_block<T, G, kHeadThreads>(sbase, num_pages, num_pages, k_sel, last_page,
+  topk_select_block<T, G, kHeadThreads>(sbase, stride, r.count, r.k, r.last_page,
                                         page_indices + b * pisb + kvh * pish, lds_keys,
-                                        keep_keys ? num_pages : 0, keep_keys);
+                                        keep_keys ? r.count : 0, keep_keys);
 }
 
 template <typename T, int LPR, int G>
 __global__ __launch_bounds__(kThreads) void criticality_kernel(
     const T* __restrict__ q, int64_t qsb, int64_t qsh, const T* __restrict__ kmin,
     const T* __restrict__ kmax, int64_t ssb, int64_t ssh, int64_t ssp,
-    const float* __restrict__ slopes, T* __restrict__ scores, int H, int Hkv, int num_pages,
-    int page_size, int seq_len, int q_pos) {
+    const float* __restrict__ slopes, T* __restrict__ scores, int H, int Hkv, int stride,
+    int page_size, int seq_len_all, int q_pos_all, const int32_t* __restrict__ seq_lens) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int SEGS = kThreads / LPR;
   const int seg = threadIdx.x / LPR;
@@ -79,6 +86,8 @@ __global__ __launch_bounds__(kThreads) void criticality_kernel(
   const int bkv = blockIdx.y;
   const int b = bkv / Hkv, kvh = bkv % Hkv;
   const int h0 = kvh * G;
+  const Ragged r = ragged_topk(seq_lens, b, page_size, stride, seq_len_all, q_pos_all, -1, -1);
+  const int num_pages = r.count, seq_len = r.seq_len, q_pos = r.q_pos;
   uint4 qraw[G], qmask[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -97,7 +106,7 @@ __global__ __launch_bounds__(kThreads) void criticality_kernel(
       hi[u] = ld16(kmx + (int64_t)p * ssp + col);
     }
   }
-  T* sbase = scores + ((int64_t)b * H + h0) * num_pages;
+  T* sbase = scores + ((int64_t)b * H + h0) * stride;
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int p = p_base + u * SEGS;
@@ -110,7 +119,7 @@ __global__ __launch_bounds__(kThreads) void criticality_kernel(
           const int last_pos = min((p + 1) * page_size - 1, seq_len - 1);
           acc = add_rn(acc, mul_rn(slopes[h0 + g], (float)(last_pos - q_pos)));
         }
-        sbase[(int64_t)g * num_pages + p] = from_f<T>(acc);
+        sbase[(int64_t)g * stride + p] = from_f<T>(acc);
       }
     }
   }
@@ -118,16 +127,18 @@ __global__ __launch_bounds__(kThreads) void criticality_kernel(
 
 template <typename T, int G>
 __global__ __launch_bounds__(kThreads) void topk_kernel(const T* __restrict__ scores, int H, int Hkv,
-                                                        int num_pages, int k, int last_page,
+                                                        int stride, int k, int last_page,
+                                                        int page_size,
+                                                        const int32_t* __restrict__ seq_lens,
                                                         int32_t* page_indices, int64_t pisb,
                                                         int64_t pish, int lds_key_cap) {
   const int bkv = blockIdx.x;
   const int b = bkv / Hkv, kvh = bkv % Hkv;
-  const T* s0 = scores + ((int64_t)b * H + kvh * G) * num_pages;
+  const Ragged r = ragged_topk(seq_lens, b, page_size, stride, 0, 0, k, last_page);
+  const T* s0 = scores + ((int64_t)b * H + kvh * G) * stride;
   extern __shared__ uint32_t lds_keys[];
-  topk_select_block<T, G, kThreads>(s0, num_pages, num_pages, k, last_page,
-                                           page_indices + b * pisb + kvh * pish, lds_keys,
-                                           lds_key_cap);
+  topk_select_block<T, G, kThreads>(s0, stride, r.count, r.k, r.last_page,
+                                    page_indices + b * pisb + kvh * pish, lds_keys, lds_key_cap);
 }
 
 template <typename F>
@@ -148,9 +159,9 @@ extern "C" int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q
                                     int64_t s_stride_h, int64_t s_stride_page,
                                     const float* alibi_slopes, void* scores, int B, int H, int Hkv,
                                     int D, int num_pages, int page_size, int seq_len, int q_pos,
-                                    int k_select, int last_page, int32_t* page_indices,
-                                    int64_t pi_stride_b, int64_t pi_stride_h, int dtype,
-                                    void* stream) {
+                                    int k_select, int last_page, const int32_t* seq_lens,
+                                    int32_t* page_indices, int64_t pi_stride_b,
+                                    int64_t pi_stride_h, int dtype, void* stream) {
   EKV_REQUIRE(q && kmin && kmax && scores, "ekv_page_criticality: null pointer");
   EKV_REQUIRE(B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0, "ekv_page_criticality: bad head counts");
   EKV_REQUIRE(num_pages >= 0 && page_size > 0, "ekv_page_criticality: bad page counts");
@@ -172,8 +183,8 @@ extern "C" int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q
                              dim3(kHeadThreads), (size_t)cap * sizeof(uint32_t), s, (const T*)q,
                              q_stride_b, q_stride_h, (const T*)kmin, (const T*)kmax, s_stride_b,
                              s_stride_h, s_stride_page, alibi_slopes, (T*)scores, H, Hkv, num_pages,
-                             page_size, seq_len, q_pos, k_select, last_page, page_indices,
-                             pi_stride_b, pi_stride_h, cap);
+                             page_size, seq_len, q_pos, k_select, last_page, seq_lens,
+                             page_indices, pi_stride_b, pi_stride_h, cap);
           return check_launch("criticality_head_kernel");
         }
         // few heads: spread the pages of each head over many workgroups, then
@@ -183,15 +194,15 @@ extern "C" int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q
         hipLaunchKernelGGL((criticality_kernel<T, LPR, G>), grid, dim3(kThreads), 0, s, (const T*)q,
                            q_stride_b, q_stride_h, (const T*)kmin, (const T*)kmax, s_stride_b,
                            s_stride_h, s_stride_page, alibi_slopes, (T*)scores, H, Hkv, num_pages,
-                           page_size, seq_len, q_pos);
+                           page_size, seq_len, q_pos, seq_lens);
         if (k_select >= 0) {
           int rc = check_launch("criticality_kernel");
           if (rc) return rc;
           const int cap2 = num_pages <= kMaxStagedKeys ? num_pages : 0;
           hipLaunchKernelGGL((topk_kernel<T, G>), dim3(B * Hkv), dim3(kThreads),
                              (size_t)cap2 * sizeof(uint32_t), s, (const T*)scores, H, Hkv,
-                             num_pages, k_select, last_page, page_indices, pi_stride_b,
-                             pi_stride_h, cap2);
+                             num_pages, k_select, last_page, page_size, seq_lens, page_indices,
+                             pi_stride_b, pi_stride_h, cap2);
           return check_launch("topk_kernel");
         }
         return check_launch("criticality_kernel");
@@ -215,7 +226,7 @@ extern "C" int ekv_topk_pages(const void* scores, int B, int H, int Hkv, int num
       const int cap = num_pages <= kMaxStagedKeys ? num_pages : 0;
       hipLaunchKernelGGL((topk_kernel<T, G>), dim3(B * Hkv), dim3(kThreads),
                          (size_t)cap * sizeof(uint32_t), s, (const T*)scores, H, Hkv, num_pages, k,
-                         last_page, page_indices, pi_stride_b, pi_stride_h, cap);
+                         last_page, 1, nullptr, page_indices, pi_stride_b, pi_stride_h, cap);
       return check_launch("topk_kernel");
     });
   });

@@ -712,6 +712,7 @@ struct SelectArgs {
   int k;              // pages selected per (b, kv head)
   int last_page;      // appended at slot k (the sentinel), or -1
   int key_cap;        // page keys that fit the dynamic LDS
+  const int32_t* seq_lens;  // [B] per-sequence lengths (ragged batch) or null
 };
 
 // One (b, kv head) per workgroup end to end: criticality scan of every page,
@@ -735,17 +736,19 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
   const int bkv = blockIdx.x;
   const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
   uint32_t* keys = reinterpret_cast<uint32_t*>(stage);
-  const bool keep = t.num_pages <= t.key_cap;
+  const topk::Ragged r = topk::ragged_topk(t.seq_lens, b, a.page_size, t.num_pages, t.seq_len,
+                                           t.q_pos, t.k, t.last_page);
+  const bool keep = r.count <= t.key_cap;
   EKV_STAMP(0);
   const T* sbase = topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC>(
       (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
-      a.slopes, (T*)t.scores, a.H, t.num_pages, a.page_size, t.seq_len, t.q_pos, b, kvh,
+      a.slopes, (T*)t.scores, a.H, t.num_pages, r.count, a.page_size, r.seq_len, r.q_pos, b, kvh,
       keep ? keys : nullptr);
   __syncthreads();
   EKV_STAMP(1);
   int32_t* pi = const_cast<int32_t*>(a.page_indices) + b * a.pisb + kvh * a.pish;
-  topk::topk_select_block<T, G, kHeadThreads>(sbase, t.num_pages, t.num_pages, t.k, t.last_page,
-                                              pi, keys, keep ? t.num_pages : 0, keep, s_pages);
+  topk::topk_select_block<T, G, kHeadThreads>(sbase, t.num_pages, r.count, r.k, r.last_page, pi,
+                                              keys, keep ? r.count : 0, keep, s_pages);
   __syncthreads();
   EKV_STAMP(2);
   const int n = token_count(a, b, kvh);
@@ -816,13 +819,15 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
     x.x = __shfl(x.x, 0);
     x.y = __shfl(x.y, 0);
     x.z = __shfl(x.z, 0);
-    const gauss::Moments m = gauss::finalize_moments(x, sel.pages);
+    const gauss::TauGeom tg = gauss::tau_geom(sel.seq_lens, b, sel.page_size, sel.pages,
+                                              f.n_tokens, f.log_n_factor);
+    const gauss::Moments m = gauss::finalize_moments(x, tg.pages);
     EKV_STAMP(7);
     const float th = f.tau_hat_given
                          ? f.tau_hat[h]
-                         : gauss::solve_single_gaussian_wave(m.mu_g, m.sigma_g, f.n_tokens,
-                                                             f.tau_alpha, f.log_n_factor,
-                                                             f.tau_iters, f.tol);
+                         : gauss::solve_single_gaussian_wave(m.mu_g, m.sigma_g, tg.n,
+                                                             f.tau_alpha, tg.lnf, f.tau_iters,
+                                                             f.tol);
     if (lane == 0) {
       s_th[wid] = th;
       s_sg[wid] = m.sigma_g;
@@ -842,7 +847,11 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
       float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
       if (ok && j < f.splits) x = f.partials[(int64_t)h * f.splits + j];
       x = gauss::reduce_splits(x, s2);
-      if (ok && j == 0) ssum += gauss::finalize_moments(x, sel.pages).sigma_g;
+      if (ok && j == 0) {
+        const int hp = sel.seq_lens ? seq_pages(sel.seq_lens[h / a.H], sel.page_size).stat_pages
+                                    : sel.pages;
+        ssum += gauss::finalize_moments(x, hp).sigma_g;
+      }
     }
     ssum = wave_sum(ssum);
     if (lane == 0) scratch[wid] = ssum;
@@ -862,7 +871,9 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
 
   // compacted length max(count - 1, 0) * ps + last_page_size; an empty table
   // attends to nothing
-  int n = count > 0 ? (count - 1) * sel.page_size + sel.last_page_size : 0;
+  const int lps = sel.seq_lens ? seq_pages(sel.seq_lens[b], sel.page_size).last_size
+                               : sel.last_page_size;
+  int n = count > 0 ? (count - 1) * sel.page_size + lps : 0;
   n = min(n, min(count * sel.page_size, a.max_tokens));
   // the first kTablePages page ids are already in s_pages
   if (n <= a.stage_cap) {

@@ -5,9 +5,8 @@
 //     one D-long row, each lane owning VEC = 16 / sizeof(T) contiguous elements
 //     (one 16-byte global load).  LPR = D / VEC is a power of two <= 64.
 //   * arithmetic is fp32; storage types are fp32, fp16 or bf16.
-//   * cross-workgroup reductions use a per-item arrival counter: the last
-//     workgroup to arrive finishes the item and resets the counter to zero, so
-//     workspaces are zeroed once at allocation and stay valid across calls.
+//   * no kernel waits for another workgroup: results that need several
+//     workgroups are combined by the next launch.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -312,51 +311,27 @@ __device__ __forceinline__ float block_sum(float x, float* scratch) {
 }
 
 // ---------------------------------------------------------------------------
-// cross-workgroup completion
+// page geometry of one sequence
 // ---------------------------------------------------------------------------
 
-// Cross-workgroup data inside one kernel goes through agent-coherent stores
-// and loads (relaxed atomics at agent scope: the stores write through to the
-// device coherence point, the loads bypass non-coherent cache levels).  This
-// avoids agent-scope fences, which on gfx950 write back and invalidate whole
-// L2 caches.
-__device__ __forceinline__ void st_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_coherent(int* p, int v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_coherent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int ld_coherent(const int* p) {
-  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_coherent_u16(uint16_t* p, uint16_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint16_t ld_coherent_u16(const uint16_t* p) {
-  return __hip_atomic_load(const_cast<uint16_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Called by every thread of a workgroup after it has issued its coherent
-// stores.  Each wave waits for its stores to complete, then one thread bumps
-// the arrival counter.  Returns true in exactly one workgroup per counter: the
-// last of `total` arrivals, which resets the counter to zero and may then read
-// every other arrival's coherent stores with ld_coherent.
-__device__ __forceinline__ bool last_arrival(int* counter, int total) {
-  __shared__ int s_last;
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = (prev == total - 1);
-    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = last;
-  }
-  __syncthreads();
-  return s_last != 0;
+// A sequence of `len` tokens in pages of `ps`: `pages` including the partial
+// last page; `stat_pages`, the pages the Gaussian statistics cover (all but
+// the last when there are two or more, gaussian_utils.py:101-102,
+// attention_gaussian.py:65-66); `stat_tokens`, the tokens of those pages
+// (seq_len_for_stats); `last_size`, the last page's token count
+// (attention_gaussian.py:79).  Top-k scores pages - 1 pages
+// (attention_topk.py:49-50).  With a batch of ragged lengths every
+// (b, kv head) workgroup derives its own geometry from seq_lens[b].
+struct SeqPages {
+  int pages, stat_pages, stat_tokens, last_size;
+};
+__host__ __device__ __forceinline__ SeqPages seq_pages(int len, int ps) {
+  SeqPages g;
+  g.pages = (len + ps - 1) / ps;
+  g.stat_pages = g.pages > 1 ? g.pages - 1 : g.pages;
+  g.stat_tokens = g.pages > 1 ? (g.pages - 1) * ps : len;
+  g.last_size = g.pages > 0 ? len - (g.pages - 1) * ps : 0;
+  return g;
 }
 
 // ---------------------------------------------------------------------------

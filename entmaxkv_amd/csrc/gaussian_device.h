@@ -40,7 +40,8 @@ inline int moment_splits(int bkv, int pages) {
 // fallback uses it.
 int launch_finalize(const void* partials, int B, int H, int Hkv, int pages, float* mu_g,
                     float* sigma_g, float* mean_var, float* var_means, float* tau_hat, float alpha,
-                    int n_tokens, int tau_iters, float tol, hipStream_t stream);
+                    int n_tokens, int tau_iters, float tol, const int32_t* seq_lens,
+                    int page_size, hipStream_t stream);
 
 __device__ __forceinline__ float normal_pdf(float x) {
   return expf(-0.5f * x * x) * 0.3989422804014327f;
@@ -201,6 +202,7 @@ struct MomentsArgs {
   float* mu_p;          // [B, H, pages]
   float* sigma_p;       // [B, H, pages]
   float4* partials;     // [B, H, splits] (Sum mu, Sum mu^2, Sum var, 0)
+  const int32_t* seq_lens;  // [B] per-sequence lengths (ragged batch) or null
 };
 
 // Moments of pages [split * pages_per_split, ...) of one (b, kv head) for its
@@ -235,8 +237,17 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
   }
   const T* km = (const T*)a.kmean + b * a.ssb + kvh * a.ssh;
   const T* ks = (const T*)a.kstd + b * a.ssb + kvh * a.ssh;
+  // ragged batch: this sequence's own statistics pages, length and position
+  int pages = a.pages, stats_len = a.stats_len, q_pos = a.q_pos;
+  if (a.seq_lens) {
+    const int len = a.seq_lens[b];
+    const SeqPages gp = seq_pages(len, a.page_size);
+    pages = min(gp.stat_pages, a.pages);
+    stats_len = gp.stat_tokens;
+    q_pos = len - 1;
+  }
   const int p_begin = split * a.pages_per_split;
-  const int p_end = min(a.pages, p_begin + a.pages_per_split);
+  const int p_end = min(pages, p_begin + a.pages_per_split);
   float s_mu[G], s_mu2[G], s_var[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) s_mu[g] = s_mu2[g] = s_var[g] = 0.f;
@@ -276,8 +287,8 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
           if (a.slopes) {
             // gaussian_utils.py:142-153: slope * (min(p*ps + (ps-1)/2, S'-1) - q_pos)
             const float pos = fminf((float)p * (float)a.page_size + (float)(a.page_size - 1) * 0.5f,
-                                    (float)(a.stats_len - 1));
-            mub = add_rn(mu, mul_rn(a.slopes[h0 + g], sub_rn(pos, (float)a.q_pos)));
+                                    (float)(stats_len - 1));
+            mub = add_rn(mu, mul_rn(a.slopes[h0 + g], sub_rn(pos, (float)q_pos)));
           }
           a.mu_p[o] = mub;
           a.sigma_p[o] = sqrtf(var);
@@ -381,7 +392,27 @@ struct SelectArgs {
   float z_clamp;
   float eps;
   float* eff;              // [2] = (safety_margin_z, max_quantile) or null
+  const int32_t* seq_lens; // [B] per-sequence lengths (ragged batch) or null; `pages`
+                           // and `num_pages` are then the longest sequence's
 };
+
+// Per-head scalars of the single-Gaussian tau-hat for batch element b: the
+// statistics pages, n = seq_len_for_stats and sqrt(2 ln(n + 1)).
+struct TauGeom {
+  int pages;
+  float n, lnf;
+};
+__device__ __forceinline__ TauGeom tau_geom(const int32_t* seq_lens, int b, int ps, int pages,
+                                            float n, float lnf) {
+  TauGeom t{pages, n, lnf};
+  if (seq_lens) {
+    const SeqPages gp = seq_pages(seq_lens[b], ps);
+    t.pages = gp.stat_pages;
+    t.n = (float)gp.stat_tokens;
+    t.lnf = (float)sqrt(2.0 * log((double)gp.stat_tokens + 1.0));
+  }
+  return t;
+}
 
 // Selects the pages of one (b, kv head) given each query head's tau-hat
 // (`tau_hat[g]`), sigma_g (`sig_g[g]`) and the batch-wide mean sigma_g
@@ -401,6 +432,14 @@ __device__ __forceinline__ int select_pack_block(const SelectArgs& a, int b, int
   const int tid = threadIdx.x;
   const int bkv = b * a.Hkv + kvh;
   const int h0 = kvh * G;
+  // this sequence's pages (ragged batch) within rows of stride a.pages
+  int pages = a.pages, num_pages = a.num_pages, last_page_size = a.last_page_size;
+  if (a.seq_lens) {
+    const SeqPages gp = seq_pages(a.seq_lens[b], a.page_size);
+    pages = min(gp.stat_pages, a.pages);
+    num_pages = min(gp.pages, a.num_pages);
+    last_page_size = gp.last_size;
+  }
 
   float smz = a.smz, z_page = a.z_page;
   if (a.auto_margins) {
@@ -422,8 +461,8 @@ __device__ __forceinline__ int select_pack_block(const SelectArgs& a, int b, int
     mu[g] = a.mu_p + ((int64_t)b * a.H + h) * a.pages;
     sg[g] = a.sigma_p + ((int64_t)b * a.H + h) * a.pages;
     float s = 0.f;
-    for (int p = tid; p < a.pages; p += NT) s += fma_rn(1.5f, sg[g][p], mu[g][p]);
-    const float upper = block_sum(s, scratch) / (float)a.pages;
+    for (int p = tid; p < pages; p += NT) s += fma_rn(1.5f, sg[g][p], mu[g][p]);
+    const float upper = block_sum(s, scratch) / (float)pages;
     const float th = tau_hat[g];
     const float thr = th / a.am1;
     const float sig_delta = smz * sig_g[g];
@@ -440,10 +479,10 @@ __device__ __forceinline__ int select_pack_block(const SelectArgs& a, int b, int
   for (int g = 0; g < G; ++g) capmax[g] = -INFINITY;
   int32_t* out = a.page_indices + b * a.pisb + kvh * a.pish;
   int base = 0;
-  for (int c0 = 0; c0 < a.pages; c0 += NT) {
+  for (int c0 = 0; c0 < pages; c0 += NT) {
     const int p = c0 + tid;
     bool sel = false;
-    if (p < a.pages) {
+    if (p < pages) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const float m = mu[g][p], s = sg[g][p];
@@ -466,16 +505,16 @@ __device__ __forceinline__ int select_pack_block(const SelectArgs& a, int b, int
     base += tot;
   }
   int count = base;
-  if (a.num_pages > a.pages) {
+  if (num_pages > pages) {
     if (tid == 0) {
-      out[base] = a.num_pages - 1;
-      if (base < lds_cap) lds_pages[base] = a.num_pages - 1;
+      out[base] = num_pages - 1;
+      if (base < lds_cap) lds_pages[base] = num_pages - 1;
     }
     count = base + 1;
   }
   if (tid == 0) {
     a.counts[bkv] = count;
-    if (a.cache_seqlens) a.cache_seqlens[bkv] = max(count - 1, 0) * a.page_size + a.last_page_size;
+    if (a.cache_seqlens) a.cache_seqlens[bkv] = max(count - 1, 0) * a.page_size + last_page_size;
   }
   // clamp: tau = min(tau_hat, max((alpha-1) * max cap over the selection - eps, floor))
 #pragma unroll

@@ -46,9 +46,11 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const float4* partia
                                                             float* var_means, float* tau_hat,
                                                             float alpha, float n_tokens,
                                                             float log_n_factor, int iters,
-                                                            float tol) {
+                                                            float tol, const int32_t* seq_lens,
+                                                            int page_size, int H) {
   const int head = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
   if (head >= count) return;
+  const TauGeom tg = tau_geom(seq_lens, head / H, page_size, pages, n_tokens, log_n_factor);
   const int lane = threadIdx.x & 63;
   const int s2 = split_lanes(splits);
   float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -58,10 +60,9 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const float4* partia
   x.x = __shfl(x.x, 0);
   x.y = __shfl(x.y, 0);
   x.z = __shfl(x.z, 0);
-  const Moments m = finalize_moments(x, pages);
+  const Moments m = finalize_moments(x, tg.pages);
   float th = 0.f;
-  if (tau_hat)
-    th = solve_single_gaussian_wave(m.mu_g, m.sigma_g, n_tokens, alpha, log_n_factor, iters, tol);
+  if (tau_hat) th = solve_single_gaussian_wave(m.mu_g, m.sigma_g, tg.n, alpha, tg.lnf, iters, tol);
   if (lane == 0) {
     mu_g[head] = m.mu_g;
     sigma_g[head] = m.sigma_g;
@@ -99,12 +100,17 @@ __device__ void mixture_eval(const float* __restrict__ mu, const float* __restri
 }
 
 __global__ __launch_bounds__(kThreads) void tau_mixture_kernel(const float* mu_p, const float* sigma_p,
-                                                               float* out, int pages, float cnt,
-                                                               float alpha, int iters, float tol) {
+                                                               float* out, int stride, float cnt,
+                                                               float alpha, int iters, float tol,
+                                                               const int32_t* seq_lens,
+                                                               int rows_per_seq, int page_size) {
   __shared__ float scratch[16];
   const int row = blockIdx.x;
-  const float* mu = mu_p + (int64_t)row * pages;
-  const float* sg = sigma_p + (int64_t)row * pages;
+  const float* mu = mu_p + (int64_t)row * stride;
+  const float* sg = sigma_p + (int64_t)row * stride;
+  // a ragged batch mixes only this sequence's statistics pages
+  const int pages =
+      seq_lens ? min(seq_pages(seq_lens[row / rows_per_seq], page_size).stat_pages, stride) : stride;
   const float a = alpha - 1.0f;
   float my = -INFINITY, ms = 0.f;
   for (int p = threadIdx.x; p < pages; p += blockDim.x) {
@@ -243,14 +249,15 @@ int dispatch_group(int G, F&& f) {
 int ekv::gauss::launch_finalize(const void* partials, int B, int H, int Hkv, int pages,
                                 float* mu_g, float* sigma_g, float* mean_var, float* var_means,
                                 float* tau_hat, float alpha, int n_tokens, int tau_iters, float tol,
-                                hipStream_t stream) {
+                                const int32_t* seq_lens, int page_size, hipStream_t stream) {
   const int count = B * H;
   const float al = fabsf(alpha - 4.0f / 3.0f) < 1e-6f ? 4.0f / 3.0f : alpha;
   const float lnf = (float)sqrt(2.0 * log((double)n_tokens + 1.0));
   hipLaunchKernelGGL(finalize_kernel, dim3((count + kThreads / 64 - 1) / (kThreads / 64)),
                      dim3(kThreads), 0, stream, (const float4*)partials,
                      moment_splits(B * Hkv, pages), pages, count, mu_g, sigma_g, mean_var,
-                     var_means, tau_hat, al, (float)n_tokens, lnf, tau_iters, tol);
+                     var_means, tau_hat, al, (float)n_tokens, lnf, tau_iters, tol, seq_lens,
+                     page_size, H);
   return check_launch("finalize_kernel");
 }
 
@@ -265,9 +272,9 @@ extern "C" int64_t ekv_gaussian_workspace_bytes(int B, int H, int Hkv, int D, in
 extern "C" int ekv_gaussian_moments(
     const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kmean, const void* kstd,
     int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, int pages_for_stats,
-    const float* alibi_slopes, int page_size, int seq_len, int n_tokens, float* mu_p,
-    float* sigma_p, int B, int H, int Hkv, int D, void* workspace, int64_t workspace_bytes,
-    int dtype, void* stream) {
+    const float* alibi_slopes, int page_size, int seq_len, int n_tokens, const int32_t* seq_lens,
+    float* mu_p, float* sigma_p, int B, int H, int Hkv, int D, void* workspace,
+    int64_t workspace_bytes, int dtype, void* stream) {
   EKV_REQUIRE(q && kmean && kstd && mu_p && sigma_p && workspace,
               "ekv_gaussian_moments: null pointer");
   EKV_REQUIRE(B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0, "ekv_gaussian_moments: bad heads");
@@ -296,6 +303,7 @@ extern "C" int ekv_gaussian_moments(
   a.mu_p = mu_p;
   a.sigma_p = sigma_p;
   a.partials = (float4*)workspace;
+  a.seq_lens = seq_lens;
   hipStream_t s = (hipStream_t)stream;
   return dispatch_dtype(dtype, [&](auto tv) {
     using T = decltype(tv);
@@ -316,18 +324,19 @@ extern "C" int ekv_gaussian_page_stats(
     int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, int pages_for_stats,
     const float* alibi_slopes, int page_size, int seq_len, float* mu_p, float* sigma_p, float* mu_g,
     float* sigma_g, float* mean_var, float* var_means, float* tau_hat, float alpha, int n_tokens,
-    int tau_iters, float tol, int B, int H, int Hkv, int D, void* workspace,
-    int64_t workspace_bytes, int dtype, void* stream) {
+    int tau_iters, float tol, const int32_t* seq_lens, int B, int H, int Hkv, int D,
+    void* workspace, int64_t workspace_bytes, int dtype, void* stream) {
   EKV_REQUIRE(mu_g && sigma_g && mean_var && var_means, "ekv_gaussian_page_stats: null pointer");
   EKV_REQUIRE(!tau_hat || alpha == 2.0f || alpha == 1.5f || fabsf(alpha - 4.0f / 3.0f) < 1e-6f,
               "ekv_gaussian_page_stats: tau-hat needs alpha in {2, 1.5, 4/3}");
   int rc = ekv_gaussian_moments(q, q_stride_b, q_stride_h, kmean, kstd, s_stride_b, s_stride_h,
                                 s_stride_page, pages_for_stats, alibi_slopes, page_size, seq_len,
-                                n_tokens, mu_p, sigma_p, B, H, Hkv, D, workspace, workspace_bytes,
-                                dtype, stream);
+                                n_tokens, seq_lens, mu_p, sigma_p, B, H, Hkv, D, workspace,
+                                workspace_bytes, dtype, stream);
   if (rc) return rc;
   return launch_finalize(workspace, B, H, Hkv, pages_for_stats, mu_g, sigma_g, mean_var,
-                         var_means, tau_hat, alpha, n_tokens, tau_iters, tol, (hipStream_t)stream);
+                         var_means, tau_hat, alpha, n_tokens, tau_iters, tol, seq_lens, page_size,
+                         (hipStream_t)stream);
 }
 
 extern "C" int ekv_tau_single_gaussian(const float* mu_g, const float* sigma_g, float* tau_out,
@@ -345,12 +354,16 @@ extern "C" int ekv_tau_single_gaussian(const float* mu_g, const float* sigma_g, 
 
 extern "C" int ekv_tau_page_mixture(const float* mu_p, const float* sigma_p, float* tau_out,
                                     int rows, int pages, float page_count, float alpha, int max_iter,
-                                    float tol, void* stream) {
+                                    float tol, const int32_t* seq_lens, int rows_per_seq,
+                                    int page_size, void* stream) {
   EKV_REQUIRE(mu_p && sigma_p && tau_out && rows >= 0 && pages > 0 && page_count > 0.f,
               "ekv_tau_page_mixture: bad arguments");
+  EKV_REQUIRE(!seq_lens || (rows_per_seq > 0 && page_size > 0),
+              "ekv_tau_page_mixture: ragged rows need rows_per_seq and page_size");
   if (rows == 0) return EKV_OK;
   hipLaunchKernelGGL(tau_mixture_kernel, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, mu_p,
-                     sigma_p, tau_out, pages, page_count, alpha, max_iter, tol);
+                     sigma_p, tau_out, pages, page_count, alpha, max_iter, tol, seq_lens,
+                     rows_per_seq, page_size);
   return check_launch("tau_mixture_kernel");
 }
 
@@ -361,7 +374,7 @@ extern "C" int ekv_select_gaussian_pack(
     float threshold_excess_margin_fraction, int32_t* page_indices, int64_t pi_stride_b,
     int64_t pi_stride_h, int32_t* counts, float* tau_floor, int32_t* cache_seqlens, int page_size,
     int last_page_size, float* tau_clamped, float z_clamp, float eps, float* effective_margins,
-    void* stream) {
+    const int32_t* seq_lens, void* stream) {
   EKV_REQUIRE(mu_p && sigma_p && tau_hat && sigma_g && page_indices && counts && tau_floor,
               "ekv_select_gaussian_pack: null pointer");
   EKV_REQUIRE(B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0, "ekv_select_gaussian_pack: bad heads");
@@ -394,6 +407,7 @@ extern "C" int ekv_select_gaussian_pack(
   a.z_clamp = z_clamp;
   a.eps = eps;
   a.eff = effective_margins;
+  a.seq_lens = seq_lens;
   hipStream_t s = (hipStream_t)stream;
   return dispatch_group(H / Hkv, [&](auto gv) {
     constexpr int G = decltype(gv)::value;

@@ -5,7 +5,8 @@
 // (kv_cache.py:72-116).  For page p the statistics cover cache rows
 // [p*ps, min((p+1)*ps, seq_len)): min, max, mean and the population standard
 // deviation clamped to >= 1e-6, all accumulated in fp32 and rounded once to the
-// key dtype.
+// key dtype.  With per-sequence lengths (seq_lens[b]) each batch element's
+// pages end at its own length.
 //
 // HBM: each page's rows are read twice (min/max/sum, then the centred second
 // moment); the second read hits L2 because a workgroup owns whole pages.
@@ -78,7 +79,8 @@ __device__ __forceinline__ void page_stats_one(const T* __restrict__ krow0, int6
 template <typename T, int LPR>
 __global__ __launch_bounds__(256) void page_stats_kernel(
     const T* __restrict__ k, int64_t ksb, int64_t ksh, int64_t ksr, StatsPtrs st, int64_t ssb,
-    int64_t ssh, int64_t ssp, int Hkv, int seq_len, int page_size, int page_begin, int page_end) {
+    int64_t ssh, int64_t ssp, int Hkv, int seq_len, const int32_t* __restrict__ seq_lens,
+    int page_size, int page_begin, int page_end) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int PPW = 256 / LPR;  // pages per workgroup
   const int seg = threadIdx.x / LPR;
@@ -88,7 +90,8 @@ __global__ __launch_bounds__(256) void page_stats_kernel(
   const int bh = blockIdx.y;
   const int b = bh / Hkv, h = bh % Hkv;
   const int r0 = page * page_size;
-  const int n_rows = min(page_size, seq_len - r0);
+  const int len = seq_lens ? seq_lens[b] : seq_len;
+  const int n_rows = min(page_size, len - r0);
   if (n_rows <= 0) return;
   const T* krow0 = k + b * ksb + h * ksh + (int64_t)r0 * ksr;
   const int64_t so = b * ssb + h * ssh + (int64_t)page * ssp;
@@ -185,12 +188,12 @@ __global__ __launch_bounds__(64) void append_kernel(
 
 template <typename T, int LPR>
 int launch_stats(const void* k, int64_t ksb, int64_t ksh, int64_t ksr, StatsPtrs st, int64_t ssb,
-                 int64_t ssh, int64_t ssp, int B, int Hkv, int seq_len, int ps, int p0, int p1,
-                 hipStream_t s) {
+                 int64_t ssh, int64_t ssp, int B, int Hkv, int seq_len, const int32_t* seq_lens,
+                 int ps, int p0, int p1, hipStream_t s) {
   constexpr int PPW = 256 / LPR;
   dim3 grid((p1 - p0 + PPW - 1) / PPW, B * Hkv);
   hipLaunchKernelGGL((page_stats_kernel<T, LPR>), grid, dim3(256), 0, s, (const T*)k, ksb, ksh,
-                     ksr, st, ssb, ssh, ssp, Hkv, seq_len, ps, p0, p1);
+                     ksr, st, ssb, ssh, ssp, Hkv, seq_len, seq_lens, ps, p0, p1);
   return check_launch("page_stats_kernel");
 }
 
@@ -211,8 +214,9 @@ int launch_append(const void* kn, const void* vn, int64_t nsb, int64_t nsh, void
 extern "C" int ekv_page_stats(const void* k, int64_t k_stride_b, int64_t k_stride_h,
                               int64_t k_stride_row, void* kmin, void* kmax, void* kmean, void* kstd,
                               int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, int B,
-                              int Hkv, int D, int seq_len, int page_size, int page_begin,
-                              int page_end, int dtype, void* stream) {
+                              int Hkv, int D, int seq_len, const int32_t* seq_lens,
+                              int page_size, int page_begin, int page_end, int dtype,
+                              void* stream) {
   EKV_REQUIRE(k && kmin && kmax && kmean && kstd, "ekv_page_stats: null pointer");
   EKV_REQUIRE(B > 0 && Hkv > 0 && page_size > 0 && seq_len >= 0, "ekv_page_stats: bad sizes");
   EKV_REQUIRE(page_begin >= 0 && page_end >= page_begin, "ekv_page_stats: bad page range");
@@ -226,7 +230,8 @@ extern "C" int ekv_page_stats(const void* k, int64_t k_stride_b, int64_t k_strid
     return dispatch_lpr<T>(D, [&](auto lpr) {
       return launch_stats<T, decltype(lpr)::value>(k, k_stride_b, k_stride_h, k_stride_row, st,
                                                    s_stride_b, s_stride_h, s_stride_page, B, Hkv,
-                                                   seq_len, page_size, page_begin, page_end, s);
+                                                   seq_len, seq_lens, page_size, page_begin,
+                                                   page_end, s);
     });
   });
 }

@@ -123,10 +123,10 @@ extern "C" int ekv_topk_paged_entmax_decode(
     int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
     int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h,
     const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
-    const int32_t* q_seqlens, const float* alibi_slopes, float* tau, int niter, void* out,
-    int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale, int page_size, int B,
-    int H, int Hkv, int D, int splits, int max_tokens, void* workspace, int64_t workspace_bytes,
-    int dtype, void* stream) {
+    const int32_t* q_seqlens, const float* alibi_slopes, const int32_t* seq_lens, float* tau,
+    int niter, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale,
+    int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens, void* workspace,
+    int64_t workspace_bytes, int dtype, void* stream) {
   EKV_REQUIRE(q && kmin && kmax && scores && k && v && page_indices && cache_seqlens && tau &&
                   out && workspace,
               "ekv_topk_paged_entmax_decode: null pointer");
@@ -143,8 +143,8 @@ extern "C" int ekv_topk_paged_entmax_decode(
   auto two_launches = [&]() {
     int rc = ekv_page_criticality(q, q_stride_b, q_stride_h, kmin, kmax, s_stride_b, s_stride_h,
                                   s_stride_page, alibi_slopes, scores, B, H, Hkv, D, num_pages,
-                                  page_size, seq_len, q_pos, k_select, last_page, page_indices,
-                                  pi_stride_b, pi_stride_h, dtype, stream);
+                                  page_size, seq_len, q_pos, k_select, last_page, seq_lens,
+                                  page_indices, pi_stride_b, pi_stride_h, dtype, stream);
     if (rc) return rc;
     return ekv_paged_entmax_decode(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h,
                                    kv_stride_row, kv_rows, page_indices, pi_stride_b, pi_stride_h,
@@ -179,6 +179,7 @@ extern "C" int ekv_topk_paged_entmax_decode(
   t.k = k_select;
   t.last_page = last_page;
   t.key_cap = num_pages;
+  t.seq_lens = seq_lens;
   hipStream_t s = (hipStream_t)stream;
   int handled = 0;
   const int rc = dispatch_dtype(dtype, [&](auto tv) {
@@ -202,9 +203,10 @@ extern "C" int ekv_gaussian_paged_entmax_decode(
     float z_clamp, float eps, float* effective_margins, const void* q, int64_t q_stride_b,
     int64_t q_stride_h, const void* k, const void* v, int64_t kv_stride_b, int64_t kv_stride_h,
     int64_t kv_stride_row, int64_t kv_rows, const int32_t* q_seqlens, const float* alibi_slopes,
-    float* tau, int tau_mode, int iters, void* out, int64_t out_stride_b, int64_t out_stride_h,
-    float alpha, float qscale, int page_size, int B, int H, int Hkv, int D, int max_tokens,
-    void* workspace, int64_t workspace_bytes, int dtype, void* stream) {
+    const int32_t* seq_lens, float* tau, int tau_mode, int iters, void* out,
+    int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale, int page_size, int B,
+    int H, int Hkv, int D, int max_tokens, void* workspace, int64_t workspace_bytes, int dtype,
+    void* stream) {
   EKV_REQUIRE(moments_workspace && mu_p && sigma_p && mu_g && sigma_g && mean_var && var_means &&
                   tau_hat && page_indices && counts && tau_floor && cache_seqlens && q && k &&
                   v && tau && out && workspace,
@@ -231,14 +233,14 @@ extern "C" int ekv_gaussian_paged_entmax_decode(
     // few heads: moments, selection and a split decode as separate launches
     int rc = gauss::launch_finalize(moments_workspace, B, H, Hkv, pages_for_stats, mu_g, sigma_g,
                                     mean_var, var_means, tau_hat_given ? nullptr : tau_hat, alpha,
-                                    n_tokens, tau_iters, tol, s);
+                                    n_tokens, tau_iters, tol, seq_lens, page_size, s);
     if (rc) return rc;
     rc = ekv_select_gaussian_pack(mu_p, sigma_p, tau_hat, sigma_g, B, H, Hkv, pages_for_stats,
                                   num_pages, alpha, auto_margins, safety_margin_z, z_page,
                                   z_page_low, z_page_high, threshold_excess_margin_fraction,
                                   page_indices, pi_stride_b, pi_stride_h, counts, tau_floor,
                                   cache_seqlens, page_size, last_page_size, tau_clamped, z_clamp,
-                                  eps, effective_margins, stream);
+                                  eps, effective_margins, seq_lens, stream);
     if (rc) return rc;
     return ekv_paged_entmax_decode(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h,
                                    kv_stride_row, kv_rows, page_indices, pi_stride_b, pi_stride_h,
@@ -282,6 +284,7 @@ extern "C" int ekv_gaussian_paged_entmax_decode(
   sel.z_clamp = z_clamp;
   sel.eps = eps;
   sel.eff = effective_margins;
+  sel.seq_lens = seq_lens;
   f.partials = (const float4*)moments_workspace;
   f.splits = gauss::moment_splits(B * Hkv, pages_for_stats);
   f.mu_g = mu_g;

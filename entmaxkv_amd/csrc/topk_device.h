@@ -22,6 +22,37 @@ constexpr int kMaxStagedKeys = 16384;
 // Batch * kv heads from which one workgroup per head fills the GPU.
 constexpr int kHeadPathMinHeads = 128;
 
+// Top-k geometry of batch element b.  With per-sequence lengths, sequence b
+// scores its pages [0, P_b - 1) (the partial last page excluded), selects
+// min(k, P_b - 1) of them and, when the caller asks for the sentinel
+// (last_page >= 0), appends its own last page P_b - 1 (attention_topk.py:
+// 49-71 per sequence); seq_len / q_pos of the ALiBi bonus are its own.
+// Without lengths, the uniform values.  `stride` is the score row stride
+// (the longest sequence's scored pages).
+struct Ragged {
+  int count, k, last_page, seq_len, q_pos;
+};
+__device__ __forceinline__ Ragged ragged_topk(const int32_t* seq_lens, int b, int ps, int stride,
+                                              int seq_len, int q_pos, int k, int last_page) {
+  Ragged r;
+  if (!seq_lens) {
+    r.count = stride;
+    r.k = k;
+    r.last_page = last_page;
+    r.seq_len = seq_len;
+    r.q_pos = q_pos;
+    return r;
+  }
+  const int len = seq_lens[b];
+  const int pages = (len + ps - 1) / ps;
+  r.count = min(max(pages - 1, 0), stride);
+  r.k = k < 0 ? k : min(k, r.count);
+  r.last_page = last_page < 0 ? last_page : pages - 1;
+  r.seq_len = len;
+  r.q_pos = len - 1;
+  return r;
+}
+
 // Order-preserving unsigned key of a stored score; NaN maps to the top.
 template <typename T> struct ScoreKey;
 template <> struct ScoreKey<_Float16> {
@@ -221,8 +252,8 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
 }
 
 // Criticality scan of one (b, kv head) by a workgroup of NT threads: scores
-// of the G query heads for pages [0, num_pages) written to `scores`
-// ([B, H, num_pages], query dtype) and, when `lds_keys` is non-null, the
+// of the G query heads for pages [0, count) written to `scores`
+// ([B, H, stride], query dtype; count <= stride) and, when `lds_keys` is non-null, the
 // group-max order key of every page kept there.  A row segment of LPR lanes
 // owns one page and loads its min and max rows with 16-byte loads, U pages
 // per segment in flight.  Returns the head's score base pointer.
@@ -230,7 +261,7 @@ template <typename T, int LPR, int G, int NT, int U>
 __device__ __forceinline__ T* criticality_scan_head(
     const T* __restrict__ q, int64_t qsb, int64_t qsh, const T* __restrict__ kmin,
     const T* __restrict__ kmax, int64_t ssb, int64_t ssh, int64_t ssp,
-    const float* __restrict__ slopes, T* __restrict__ scores, int H, int num_pages,
+    const float* __restrict__ slopes, T* __restrict__ scores, int H, int stride, int num_pages,
     int page_size, int seq_len, int q_pos, int b, int kvh, uint32_t* lds_keys) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int SEGS = NT / LPR;
@@ -253,7 +284,7 @@ __device__ __forceinline__ T* criticality_scan_head(
   }
   const T* kmn = kmin + b * ssb + kvh * ssh;
   const T* kmx = kmax + b * ssb + kvh * ssh;
-  T* sbase = scores + ((int64_t)b * H + h0) * num_pages;
+  T* sbase = scores + ((int64_t)b * H + h0) * stride;
 
   for (int p0 = 0; p0 < num_pages; p0 += ROUND) {
     uint4 lo[U], hi[U];
@@ -279,7 +310,7 @@ __device__ __forceinline__ T* criticality_scan_head(
         }
         const T sv = from_f<T>(acc);
         key = max(key, ScoreKey<T>::key(sv));
-        if (p < num_pages && sl == 0) sbase[(int64_t)g * num_pages + p] = sv;
+        if (p < num_pages && sl == 0) sbase[(int64_t)g * stride + p] = sv;
       }
       if (keep_keys && p < num_pages && sl == 0) lds_keys[p] = key;
     }

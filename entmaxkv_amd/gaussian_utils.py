@@ -22,11 +22,13 @@ from . import kernels as K
 def solve_for_tau_hat_page_gaussian_mixture_auto(mu_pages, sigma_pages, page_counts=None,
                                                  alpha: float = 1.5, max_iter: int = 40,
                                                  tol: float = 1e-6,
-                                                 uniform_page_count: float = 1.0):
-    """gaussian_utils.py:16-49 (always the native kernel)."""
+                                                 uniform_page_count: float = 1.0,
+                                                 seq_lens=None, page_size: int = 16):
+    """gaussian_utils.py:16-49 (always the native kernel).  With ``seq_lens`` (a
+    ragged batch, rows [B, H, ...]) row (b, h) mixes only sequence b's pages."""
     return K.solve_for_tau_hat_page_gaussian_mixture(
         mu_pages, sigma_pages, page_counts=page_counts, alpha=alpha, max_iter=max_iter, tol=tol,
-        uniform_page_count=uniform_page_count)
+        uniform_page_count=uniform_page_count, seq_lens=seq_lens, page_size=page_size)
 
 
 def compute_gaussian_aware_statistics(q, k_mean, k_std, seq_len: int, page_size: int,

@@ -49,14 +49,15 @@ def page_quantile_z(quantile: float, page_size: int) -> float:
 # ---------------------------------------------------------------------------
 
 def page_stats(k: torch.Tensor, kmin, kmax, kmean, kstd, seq_len: int, page_size: int,
-               page_begin: int, page_end: int) -> None:
-    """Fill stats for pages [page_begin, page_end) from rows of k [B, Hkv, S_cap, D]."""
+               page_begin: int, page_end: int, seq_lens: torch.Tensor | None = None) -> None:
+    """Fill stats for pages [page_begin, page_end) from rows of k [B, Hkv, S_cap, D]
+    (``seq_lens`` [B] int32: each sequence's pages end at its own length)."""
     require_gpu(k, kmin)
     B, Hkv, _, D = k.shape
     call("ekv_page_stats", k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
          kmin.data_ptr(), kmax.data_ptr(), kmean.data_ptr(), kstd.data_ptr(),
-         kmin.stride(0), kmin.stride(1), kmin.stride(2), B, Hkv, D, seq_len, page_size,
-         page_begin, page_end, dtype_code(k.dtype), stream_ptr(k.device))
+         kmin.stride(0), kmin.stride(1), kmin.stride(2), B, Hkv, D, seq_len, ptr(seq_lens),
+         page_size, page_begin, page_end, dtype_code(k.dtype), stream_ptr(k.device))
 
 
 def append_token(k_new, v_new, k, v, kmin, kmax, kmean, kstd, pos: int, page_size: int,
@@ -83,12 +84,15 @@ def append_token(k_new, v_new, k, v, kmin, kmax, kmean, kstd, pos: int, page_siz
 def estimate_page_criticality(q, k_min, k_max, alibi_slopes=None, q_pos: int = 0,
                               page_size: int = 16, seq_len: int = 0,
                               exclude_last_page: bool = False, out: torch.Tensor | None = None,
-                              topk: tuple | None = None) -> torch.Tensor:
+                              topk: tuple | None = None,
+                              seq_lens: torch.Tensor | None = None) -> torch.Tensor:
     """Upper-bound page scores [B, H, P(-1)] in the query dtype.
 
     Mirrors triton_estimate_page_criticality (kernels/page_criticality.py:107-187,
     apply_scaling=False).  ``topk=(k, last_page, page_indices)`` also produces
     the top-k page table (ekv_topk_pages semantics) in the same call.
+    ``seq_lens`` [B] (ragged batch): sequence b scores, selects and appends its
+    last page for its own length; the score rows keep the longest's stride.
     """
     require_gpu(q, k_min, k_max)
     B, H, _, D = q.shape
@@ -110,7 +114,7 @@ def estimate_page_criticality(q, k_min, k_max, alibi_slopes=None, q_pos: int = 0
     call("ekv_page_criticality", q3.data_ptr(), q3.stride(0), q3.stride(1),
          k_min.data_ptr(), k_max.data_ptr(), k_min.stride(0), k_min.stride(1), k_min.stride(2),
          ptr(slopes), out.data_ptr(), B, H, Hkv, D, num_pages, page_size, seq_len, q_pos,
-         k_sel, last_page, ptr(pidx), 0 if pidx is None else pidx.stride(0),
+         k_sel, last_page, ptr(seq_lens), ptr(pidx), 0 if pidx is None else pidx.stride(0),
          0 if pidx is None else pidx.stride(1), dtype_code(q.dtype),
          stream_ptr(q.device))
     return out
@@ -233,7 +237,8 @@ def topk_paged_entmax_decode(q, k_min, k_max, scores, k_select: int, last_page: 
                              alpha: float, niter: int, seq_len: int, q_pos: int,
                              alibi_slopes=None, q_seqlens=None,
                              workspace: DecodeWorkspace | None = None, kv_rows: int | None = None,
-                             taus_out: torch.Tensor | None = None):
+                             taus_out: torch.Tensor | None = None,
+                             seq_lens: torch.Tensor | None = None):
     """Criticality + top-k + exact-tau decode of one step (ekv_topk_paged_entmax_decode).
 
     Scores the pages [0, scores.shape[2]) into ``scores``, writes the top-k page
@@ -287,7 +292,8 @@ def topk_paged_entmax_decode(q, k_min, k_max, scores, k_select: int, last_page: 
          k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), kv_rows,
          page_indices.data_ptr(), page_indices.stride(0), page_indices.stride(1),
          cache_seqlens.data_ptr(), cache_seqlens.stride(0), cache_seqlens.stride(1),
-         ptr(qsl), ptr(slopes), tau.data_ptr(), niter, o_target.data_ptr(), o_target.stride(0),
+         ptr(qsl), ptr(slopes), ptr(seq_lens), tau.data_ptr(), niter, o_target.data_ptr(),
+         o_target.stride(0),
          o_target.stride(1), float(alpha), qscale_for(alpha, dim, q.dtype), page_size, batch,
          nheads, num_kv_heads, dim, workspace.splits, workspace.max_tokens,
          workspace.buf.data_ptr(), workspace.buf.numel(), dtype_code(q.dtype),
@@ -354,7 +360,8 @@ class GaussianBuffers:
 def compute_page_gaussian_stats(q, k_mean, k_std, pages_for_stats, *, alibi_slopes=None,
                                 page_size=16, seq_len=0, alpha=1.5, n_tokens=None,
                                 solve_tau=True, tau_iters=120, tol=1e-6,
-                                buffers: GaussianBuffers | None = None) -> GaussianBuffers:
+                                buffers: GaussianBuffers | None = None,
+                                seq_lens: torch.Tensor | None = None) -> GaussianBuffers:
     """Per-page score moments, global moments and (optionally) the fused tau-hat.
 
     Mirrors compute_page_gaussian_stats_triton (kernels/gaussian_page_stats.py:128-233,
@@ -391,7 +398,8 @@ def compute_page_gaussian_stats(q, k_mean, k_std, pages_for_stats, *, alibi_slop
          buffers.mu_p.data_ptr(), buffers.sigma_p.data_ptr(), buffers.mu_g.data_ptr(),
          buffers.sigma_g.data_ptr(), buffers.mean_var.data_ptr(), buffers.var_means.data_ptr(),
          buffers.tau_hat.data_ptr() if solve_tau else None, float(alpha), int(n_tokens),
-         int(tau_iters), float(tol), B, H, Hkv, D, buffers.ws.data_ptr(), buffers.ws.numel(),
+         int(tau_iters), float(tol), ptr(seq_lens), B, H, Hkv, D, buffers.ws.data_ptr(),
+         buffers.ws.numel(),
          dtype_code(q.dtype), stream_ptr(q.device))
     return buffers
 
@@ -407,7 +415,8 @@ def _alibi_f32(alibi_slopes, device):
 
 def compute_page_gaussian_moments(q, k_mean, k_std, pages_for_stats, buffers: GaussianBuffers, *,
                                   alibi_slopes=None, page_size=16, seq_len=0,
-                                  n_tokens=None) -> GaussianBuffers:
+                                  n_tokens=None,
+                                  seq_lens: torch.Tensor | None = None) -> GaussianBuffers:
     """Per-page moments mu_p / sigma_p and the partial sums of the global moments
     (the first launch of the Gaussian step; kernels/gaussian_page_stats.py:8-121)."""
     require_gpu(q, k_mean, k_std)
@@ -423,7 +432,7 @@ def compute_page_gaussian_moments(q, k_mean, k_std, pages_for_stats, buffers: Ga
     call("ekv_gaussian_moments", q3.data_ptr(), q3.stride(0), q3.stride(1), k_mean.data_ptr(),
          k_std.data_ptr(), k_mean.stride(0), k_mean.stride(1), k_mean.stride(2), pages_for_stats,
          ptr(_alibi_f32(alibi_slopes, q.device)), page_size, seq_len, int(n_tokens),
-         buffers.mu_p.data_ptr(), buffers.sigma_p.data_ptr(), B, H, Hkv, D, buffers.ws.data_ptr(),
+         ptr(seq_lens), buffers.mu_p.data_ptr(), buffers.sigma_p.data_ptr(), B, H, Hkv, D, buffers.ws.data_ptr(),
          buffers.ws.numel(), dtype_code(q.dtype), stream_ptr(q.device))
     return buffers
 
@@ -437,7 +446,8 @@ def gaussian_paged_entmax_decode(q, k_cache, v_cache, out, buffers: GaussianBuff
                                  clamp_quantile: float, effective, tau_out, tau_mode: int,
                                  iters: int, workspace: DecodeWorkspace, alibi_slopes=None,
                                  q_seqlens=None, kv_rows=None, eps: float = 1e-4,
-                                 tau_iters: int = 120, tol: float = 1e-6):
+                                 tau_iters: int = 120, tol: float = 1e-6,
+                                 seq_lens: torch.Tensor | None = None):
     """Selection + decode of one Gaussian-aware step after compute_page_gaussian_moments
     (ekv_gaussian_paged_entmax_decode): global moments and tau-hat (unless
     ``tau_hat_given``), threshold select + pack + clamp (``tau_clamped`` None =
@@ -476,7 +486,8 @@ def gaussian_paged_entmax_decode(q, k_cache, v_cache, out, buffers: GaussianBuff
          ptr(tau_clamped), page_quantile_z(clamp_quantile, page_size), float(eps), ptr(effective),
          q3.data_ptr(), q3.stride(0), q3.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
          k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), kv_rows, ptr(qsl),
-         ptr(_alibi_f32(alibi_slopes, q.device)), tau_out.data_ptr(), int(tau_mode), int(iters),
+         ptr(_alibi_f32(alibi_slopes, q.device)), ptr(seq_lens), tau_out.data_ptr(),
+         int(tau_mode), int(iters),
          o_target.data_ptr(), o_target.stride(0), o_target.stride(1), float(alpha),
          qscale_for(alpha, D, q.dtype), page_size, B, H, Hkv, D, workspace.max_tokens,
          workspace.buf.data_ptr(), workspace.buf.numel(), dtype_code(q.dtype),
@@ -500,7 +511,8 @@ def solve_for_tau_hat_single_gaussian_gpu(mu_g, sigma_g, n, alpha, iterations=12
 
 
 def solve_for_tau_hat_page_gaussian_mixture(mu_pages, sigma_pages, page_counts=None, alpha=1.5,
-                                            max_iter=40, tol=1e-6, uniform_page_count=1.0):
+                                            max_iter=40, tol=1e-6, uniform_page_count=1.0,
+                                            seq_lens=None, page_size=16):
     """Page-mixture tau-hat [..., 1]; mirrors kernels/tau_mixture_solver_triton.py:172-240.
 
     Per-page counts other than one uniform value are not supported by the
@@ -530,7 +542,9 @@ def solve_for_tau_hat_page_gaussian_mixture(mu_pages, sigma_pages, page_counts=N
     sg = sigma_pages.to(torch.float32).contiguous()
     out = torch.empty(rows, device=mu.device, dtype=torch.float32)
     call("ekv_tau_page_mixture", mu.data_ptr(), sg.data_ptr(), out.data_ptr(), rows, pages,
-         float(uniform_page_count), float(alpha), int(max_iter), float(tol), stream_ptr(mu.device))
+         float(uniform_page_count), float(alpha), int(max_iter), float(tol), ptr(seq_lens),
+         int(mu_pages.shape[1]) if (seq_lens is not None and mu_pages.dim() >= 3) else 1,
+         int(page_size), stream_ptr(mu.device))
     return out.view(*mu_pages.shape[:-1], 1).to(mu_pages.dtype)
 
 
@@ -539,7 +553,7 @@ def select_gaussian_threshold_pack(mu_p, sigma_p, tau_hat, sigma_g, page_size, a
                                    threshold_excess_margin_fraction, pages_for_stats, num_pages,
                                    num_kv_heads=None, out=None, counts=None, tau_floor=None,
                                    cache_seqlens=None, last_page_size=None, tau_clamped=None,
-                                   clamp_quantile=0.5, eps=1e-4, effective=None):
+                                   clamp_quantile=0.5, eps=1e-4, effective=None, seq_lens=None):
     """Threshold select + pack (+ fused lengths and tau clamp).
 
     Mirrors select_gaussian_threshold_pack_triton (kernels/selection_pack.py:201-272).
@@ -576,7 +590,7 @@ def select_gaussian_threshold_pack(mu_p, sigma_p, tau_hat, sigma_g, page_size, a
          int(auto), smz, z_page, z_low, z_high, float(threshold_excess_margin_fraction),
          out.data_ptr(), out.stride(0), out.stride(1), counts.data_ptr(), tau_floor.data_ptr(),
          ptr(cache_seqlens), page_size, last_page_size, ptr(tau_clamped), z_clamp, float(eps),
-         ptr(effective), stream_ptr(dev))
+         ptr(effective), ptr(seq_lens), stream_ptr(dev))
     return out, counts, tau_floor
 
 

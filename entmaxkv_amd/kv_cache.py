@@ -15,6 +15,11 @@ constructor, methods and attributes.  What changes is the storage:
   ``[B, Hkv, P, D]`` of them.
 * ``initialize`` computes all page statistics with one kernel launch instead
   of a Python loop over pages (kv_cache.py:58-70).
+* Ragged batches (no counterpart in the reference, whose cache holds one
+  length): ``initialize(k, v, seq_lens=...)`` gives every sequence its own
+  length.  ``seq_lens`` (device int32 [B]) then drives every kernel: each
+  sequence has its own pages, last page, statistics and append position;
+  ``seq_len`` is the longest length and fixes the buffer shapes.
 """
 
 from __future__ import annotations
@@ -39,6 +44,8 @@ class PagedKVCache:
         self.capacity = capacity
         self.headroom = headroom
         self.seq_len = 0
+        self.seq_lens: Optional[torch.Tensor] = None  # [B] int32 on the device (ragged batch)
+        self._lens_host = None
         self._k = None
         self._v = None
         self._bounds = None
@@ -89,6 +96,21 @@ class PagedKVCache:
         return self._stat(self._moments, 1)
 
     @property
+    def is_ragged(self) -> bool:
+        return self.seq_lens is not None
+
+    def compacted_seqlens(self, token_budget: int) -> torch.Tensor:
+        """Per-sequence compacted token counts of a top-k step, [B] int32 on the
+        device: min(budget // ps, P_b - 1) * ps + last_page_size_b (what the
+        reference's caller passes as ``cache_seqlens``, tests/test_topk.py:81-85)."""
+        ps = self.page_size
+        lens = self.seq_lens if self.seq_lens is not None else torch.full(
+            (self._k.shape[0],), self.seq_len, dtype=torch.int32, device=self._k.device)
+        pages = (lens + ps - 1) // ps
+        k = torch.clamp(pages - 1, min=0, max=token_budget // ps)
+        return (k * ps + lens - (pages - 1) * ps).to(torch.int32)
+
+    @property
     def kv_capacity(self) -> int:
         return 0 if self._k is None else self._k.shape[2]
 
@@ -113,24 +135,39 @@ class PagedKVCache:
         moments[:, :, :pc].copy_(self._moments)
         self._k, self._v, self._bounds, self._moments = k, v, bounds, moments
 
-    def initialize(self, k: torch.Tensor, v: torch.Tensor):
-        """Initialize the cache with prefill keys/values (kv_cache.py:40-70)."""
+    def initialize(self, k: torch.Tensor, v: torch.Tensor, seq_lens=None):
+        """Initialize the cache with prefill keys/values (kv_cache.py:40-70).
+
+        ``seq_lens`` (optional, [B] ints): sequence b holds only its first
+        seq_lens[b] rows of ``k``/``v`` (a ragged batch).
+        """
         if not k.is_cuda:
             raise ValueError("PagedKVCache requires GPU tensors")
         batch, num_heads, seq_len, head_dim = k.shape
+        self.seq_lens = None
+        self._lens_host = None
+        if seq_lens is not None:
+            host = torch.as_tensor(seq_lens, dtype=torch.int64).reshape(-1).cpu()
+            if host.numel() != batch:
+                raise ValueError(f"seq_lens has {host.numel()} entries for a batch of {batch}")
+            if bool((host < 1).any()) or bool((host > seq_len).any()):
+                raise ValueError(f"seq_lens must lie in [1, {seq_len}]")
+            self._lens_host = host
+            self.seq_lens = host.to(device=k.device, dtype=torch.int32)
+            seq_len = int(host.max())
         cap = self.capacity if self.capacity is not None else seq_len + self.headroom
         cap = max(cap, seq_len + 1)
         self._k, self._v, self._bounds, self._moments = self._allocate(
             batch, num_heads, cap, head_dim, k.dtype, k.device)
-        self._k[:, :, :seq_len].copy_(k)
-        self._v[:, :, :seq_len].copy_(v)
+        self._k[:, :, :seq_len].copy_(k[:, :, :seq_len])
+        self._v[:, :, :seq_len].copy_(v[:, :, :seq_len])
         self.seq_len = seq_len
         self._page_indices_buf = None
         self._page_indices_last_page = None
         if seq_len > 0:
             K.page_stats(self._k, self._bounds[:, :, :, 0], self._bounds[:, :, :, 1],
                          self._moments[:, :, :, 0], self._moments[:, :, :, 1], seq_len,
-                         self.page_size, 0, self.num_pages)
+                         self.page_size, 0, self.num_pages, seq_lens=self.seq_lens)
 
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor):
         """Append one token per (b, kv head) and update its page's stats (kv_cache.py:72-116).
@@ -146,8 +183,15 @@ class PagedKVCache:
             self._grow(pos + 1 + self.headroom)
         K.append_token(k_new[:, :, 0], v_new[:, :, 0], self._k, self._v,
                        self._bounds[:, :, :, 0], self._bounds[:, :, :, 1],
-                       self._moments[:, :, :, 0], self._moments[:, :, :, 1], pos, self.page_size)
-        self.seq_len = pos + 1
+                       self._moments[:, :, :, 0], self._moments[:, :, :, 1], pos, self.page_size,
+                       pos_per_batch=self.seq_lens)
+        if self.seq_lens is not None:
+            # every sequence grows by one token at its own position
+            self.seq_lens.add_(1)
+            self._lens_host += 1
+            self.seq_len = int(self._lens_host.max())
+        else:
+            self.seq_len = pos + 1
 
     # ---------------------------------------------------------- criticality
     def estimate_page_criticality(self, q: torch.Tensor, use_triton: bool = False,
@@ -160,13 +204,15 @@ class PagedKVCache:
         return K.estimate_page_criticality(
             q, self.k_min, self.k_max, alibi_slopes=alibi_slopes, q_pos=q_pos,
             page_size=self.page_size, seq_len=self.seq_len,
-            exclude_last_page=exclude_last_page)
+            exclude_last_page=exclude_last_page,
+            seq_lens=self.seq_lens if exclude_last_page else None)
 
     def select_topk(self, q: torch.Tensor, k: int, alibi_slopes=None) -> torch.Tensor:
         """Fused criticality + top-k page table [B, Hkv, k + 1] (last page at slot k).
 
         Replaces attention_topk.py:45-71.  Under GQA a kv head's page score is
-        the maximum of its query heads' scores.
+        the maximum of its query heads' scores.  In a ragged batch sequence b
+        selects k_b = min(k, P_b - 1) pages, its last page at slot k_b.
         """
         B, H = q.shape[:2]
         Hkv = self._k.shape[1]
@@ -176,11 +222,15 @@ class PagedKVCache:
         scores = self._get_scores_buf(B, H, P - 1, q.dtype, q.device)
         self.last_page_scores = scores
         if k == 0:
+            if self.seq_lens is not None:
+                # every sequence's own last page
+                last_b = (self.seq_lens + self.page_size - 1) // self.page_size - 1
+                buf[:, :, 0].copy_(last_b[:, None].expand(B, Hkv))
             return buf
         K.estimate_page_criticality(
             q, self.k_min, self.k_max, alibi_slopes=alibi_slopes, q_pos=self.seq_len - 1,
             page_size=self.page_size, seq_len=self.seq_len, exclude_last_page=True,
-            out=scores, topk=(k, last, buf))
+            out=scores, topk=(k, last, buf), seq_lens=self.seq_lens)
         return buf
 
     def _get_scores_buf(self, B, H, P, dtype, device):

@@ -3,12 +3,18 @@
  *
  * Every entry point takes raw device pointers, element strides and a
  * hipStream_t passed as void*.  Nothing here allocates device memory:
- * workspaces are caller-owned, sized by the *_workspace_bytes queries, and
- * must be zero-filled once when first allocated (arrival counters inside them
- * return to zero after every call).  Calls that share a workspace must not run
+ * workspaces are caller-owned and sized by the *_workspace_bytes queries;
+ * they need no initialisation.  Calls that share a workspace must not run
  * concurrently.  Return value: 0 on success, EKV_ERR_ARG (-1) for a rejected
  * argument (nothing launched), EKV_ERR_HIP (-2) for a launch failure; the
  * message is in ekv_last_error() (thread-local).
+ *
+ * Ragged batches: entry points with a `seq_lens` argument accept per-sequence
+ * lengths [B] (int32, device).  Sequence b then uses its own page count,
+ * last page and statistics length; the scalar sizes (seq_len, num_pages,
+ * pages_for_stats, ...) describe the longest sequence and fix the strides.
+ * Null keeps one length for the whole batch.  This has no counterpart in the
+ * reference, whose cache holds one length (kv_cache.py:23-38).
  *
  * dtype codes: 0 = fp32, 1 = fp16, 2 = bf16 (storage type of q/K/V/stats).
  * Head dim D: D / (16 / sizeof(dtype)) must be a power of two in [4, 64]
@@ -35,7 +41,8 @@ int ekv_abi_version(void);
 int ekv_page_stats(const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_row,
                    void* kmin, void* kmax, void* kmean, void* kstd, int64_t s_stride_b,
                    int64_t s_stride_h, int64_t s_stride_page, int B, int Hkv, int D, int seq_len,
-                   int page_size, int page_begin, int page_end, int dtype, void* stream);
+                   const int32_t* seq_lens, int page_size, int page_begin, int page_end,
+                   int dtype, void* stream);
 
 /* In-place append of one token per (b, kv head) at row `pos` (or
  * pos_per_batch[b] when non-null, negative = skip) and recompute of that
@@ -56,8 +63,9 @@ int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q_stride_h, 
                          const void* kmax, int64_t s_stride_b, int64_t s_stride_h,
                          int64_t s_stride_page, const float* alibi_slopes, void* scores, int B,
                          int H, int Hkv, int D, int num_pages, int page_size, int seq_len,
-                         int q_pos, int k_select, int last_page, int32_t* page_indices,
-                         int64_t pi_stride_b, int64_t pi_stride_h, int dtype, void* stream);
+                         int q_pos, int k_select, int last_page, const int32_t* seq_lens,
+                         int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h,
+                         int dtype, void* stream);
 
 /* Top-k page table per (b, kv head): the k pages with the largest score (group
  * maximum under GQA), ascending, ties to the lower index, then `last_page`
@@ -106,10 +114,10 @@ int ekv_topk_paged_entmax_decode(
     int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
     int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h,
     const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
-    const int32_t* q_seqlens, const float* alibi_slopes, float* tau, int niter, void* out,
-    int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale, int page_size, int B,
-    int H, int Hkv, int D, int splits, int max_tokens, void* workspace, int64_t workspace_bytes,
-    int dtype, void* stream);
+    const int32_t* q_seqlens, const float* alibi_slopes, const int32_t* seq_lens, float* tau,
+    int niter, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale,
+    int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens, void* workspace,
+    int64_t workspace_bytes, int dtype, void* stream);
 
 /* Workspace for ekv_gaussian_moments / ekv_gaussian_page_stats (the partial
  * sums of the global moments; needs no initialisation). */
@@ -124,9 +132,9 @@ int64_t ekv_gaussian_workspace_bytes(int B, int H, int Hkv, int D, int pages, in
 int ekv_gaussian_moments(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kmean,
                          const void* kstd, int64_t s_stride_b, int64_t s_stride_h,
                          int64_t s_stride_page, int pages_for_stats, const float* alibi_slopes,
-                         int page_size, int seq_len, int n_tokens, float* mu_p, float* sigma_p,
-                         int B, int H, int Hkv, int D, void* workspace, int64_t workspace_bytes,
-                         int dtype, void* stream);
+                         int page_size, int seq_len, int n_tokens, const int32_t* seq_lens,
+                         float* mu_p, float* sigma_p, int B, int H, int Hkv, int D,
+                         void* workspace, int64_t workspace_bytes, int dtype, void* stream);
 
 /* Per-page score moments mu_p, sigma_p [B, H, pages_for_stats] (fp32; mu_p
  * includes the ALiBi page-mean bias when alibi_slopes is non-null), per-head
@@ -140,8 +148,9 @@ int ekv_gaussian_page_stats(const void* q, int64_t q_stride_b, int64_t q_stride_
                             const float* alibi_slopes, int page_size, int seq_len, float* mu_p,
                             float* sigma_p, float* mu_g, float* sigma_g, float* mean_var,
                             float* var_means, float* tau_hat, float alpha, int n_tokens,
-                            int tau_iters, float tol, int B, int H, int Hkv, int D,
-                            void* workspace, int64_t workspace_bytes, int dtype, void* stream);
+                            int tau_iters, float tol, const int32_t* seq_lens, int B, int H,
+                            int Hkv, int D, void* workspace, int64_t workspace_bytes, int dtype,
+                            void* stream);
 
 /* tau-hat for `count` independent single-Gaussian problems.  Replaces
  * solve_for_tau_hat_single_gaussian_gpu, kernels/tau_solver_gpu.py:128-158. */
@@ -149,10 +158,13 @@ int ekv_tau_single_gaussian(const float* mu_g, const float* sigma_g, float* tau_
                             int n_tokens, float alpha, int iterations, float tol, void* stream);
 
 /* Page-mixture tau-hat per row of [rows, pages] (uniform page count).
- * Replaces solve_for_tau_hat_page_gaussian_mixture_triton,
+ * With seq_lens (ragged batch), row r mixes the statistics pages of sequence
+ * r / rows_per_seq only.  Replaces
+ * solve_for_tau_hat_page_gaussian_mixture_triton,
  * kernels/tau_mixture_solver_triton.py:172-240. */
 int ekv_tau_page_mixture(const float* mu_p, const float* sigma_p, float* tau_out, int rows,
                          int pages, float page_count, float alpha, int max_iter, float tol,
+                         const int32_t* seq_lens, int rows_per_seq, int page_size,
                          void* stream);
 
 /* Threshold selection + ascending pack + last-page sentinel per (b, kv head),
@@ -171,7 +183,7 @@ int ekv_select_gaussian_pack(const float* mu_p, const float* sigma_p, const floa
                              int64_t pi_stride_b, int64_t pi_stride_h, int32_t* counts,
                              float* tau_floor, int32_t* cache_seqlens, int page_size,
                              int last_page_size, float* tau_clamped, float z_clamp, float eps,
-                             float* effective_margins, void* stream);
+                             float* effective_margins, const int32_t* seq_lens, void* stream);
 
 /* One Gaussian-aware decode step after ekv_gaussian_moments (whose workspace
  * and mu_p / sigma_p it reads): global moments and tau-hat per head (unless
@@ -197,9 +209,10 @@ int ekv_gaussian_paged_entmax_decode(
     float z_clamp, float eps, float* effective_margins, const void* q, int64_t q_stride_b,
     int64_t q_stride_h, const void* k, const void* v, int64_t kv_stride_b, int64_t kv_stride_h,
     int64_t kv_stride_row, int64_t kv_rows, const int32_t* q_seqlens, const float* alibi_slopes,
-    float* tau, int tau_mode, int iters, void* out, int64_t out_stride_b, int64_t out_stride_h,
-    float alpha, float qscale, int page_size, int B, int H, int Hkv, int D, int max_tokens,
-    void* workspace, int64_t workspace_bytes, int dtype, void* stream);
+    const int32_t* seq_lens, float* tau, int tau_mode, int iters, void* out,
+    int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale, int page_size, int B,
+    int H, int Hkv, int D, int max_tokens, void* workspace, int64_t workspace_bytes, int dtype,
+    void* stream);
 
 /* Standalone tau clamp over a page list (kernels/tau_clamp.py:8-73). */
 int ekv_tau_clamp(const float* tau, const float* mu_p, const float* sigma_p,

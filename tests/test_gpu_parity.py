@@ -357,6 +357,38 @@ def test_topk_api_end_to_end(dtype, G, path, alibi):
     assert_out_close(to_np(out)[:, :, 0], ref, dtype)
 
 
+def test_config1_topk_step():
+    """BASELINE config 1 on the GPU: B=1, H=32, D=128, 1024-token prefill + one
+    appended token, page size 16, fp32, budget 256, alpha 1.5 (niter 10): the
+    page table equals the oracle's top-k of the kernel's scores and the output
+    equals the oracle step within 1e-5."""
+    from entmaxkv_amd import sparse_attention_decode_paged
+    _case(test="config1")
+    rng = np.random.default_rng(0)
+    B, H, S0, D, ps, budget, dtype = 1, 32, 1024, 128, 16, 256, "fp32"
+    cache, k, v = _build_cache(rng, B, H, S0, D, dtype)
+    q = randn(rng, (B, H, 1, D), dtype)
+    kn = randn(rng, (B, H, 1, D), dtype)
+    vn = randn(rng, (B, H, 1, D), dtype)
+    S = S0 + 1
+    P = (S + ps - 1) // ps
+    n_sel = budget // ps
+    out = torch.zeros(B, H, 1, D, dtype=torch.float32, device="cuda")
+    sparse_attention_decode_paged(
+        to_dev(q, dtype), cache, to_dev(kn, dtype), to_dev(vn, dtype), out, budget,
+        torch.full((B,), n_sel * ps + 1, dtype=torch.int32, device="cuda"),
+        torch.full((B,), S, dtype=torch.int32, device="cuda"), alpha=1.5, niter=10)
+    torch.cuda.synchronize()
+    Kf = np.concatenate([k, kn], axis=2)
+    Vf = np.concatenate([v, vn], axis=2)
+    scores = to_np(cache.last_page_scores)
+    pidx = np.concatenate([O.topk_pages(scores, n_sel), np.full((B, H, 1), P - 1)], axis=2)
+    np.testing.assert_array_equal(to_np(cache._page_indices_buf).astype(np.int64), pidx)
+    ref, _ = O.paged_entmax_decode(q[:, :, 0], Kf, Vf, pidx, np.full((B, H), n_sel * ps + 1), ps,
+                                   1.5, 10, dtype)
+    assert_out_close(to_np(out)[:, :, 0], ref, dtype)
+
+
 # ---------------------------------------------------------------------------
 # a7 - a12 Gaussian path
 # ---------------------------------------------------------------------------
@@ -521,6 +553,122 @@ GAUSS_FUSED_CASES = [("fp16", 1, "corrected", 1.5), ("bf16", 1, "exact", 1.5),
                      ("bf16", 2, "corrected", 2.0), ("fp16", 8, "exact", 1.5)]
 
 
+def _check_gaussian_step(cache, q, k, v, out, dtype, G, tau_mode, alpha, lens):
+    """The Gaussian step's stages against the oracle, sequence by sequence.
+
+    ``lens`` [B]: the sequence lengths (all equal for a uniform batch).  The
+    automatic margins are batch-wide, so they come from every head's sigma_g;
+    everything else is per sequence."""
+    st = cache.last_gaussian_stats
+    ps = cache.page_size
+    B, H = q.shape[:2]
+    Hkv = H // G
+    mu_p_all, sg_p_all = to_np(st["mu_scores_per_page"]), to_np(st["sigma_scores_per_page"])
+    mu_g = to_np(st["mu_global"])[..., 0]
+    sg_g = to_np(st["sigma_global"])[..., 0]
+    th = to_np(st["tau_hat"])
+    tf = to_np(st["tau_floor"])
+    eff = to_np(st["effective_margins"])
+    smz, mq = O.auto_selection_margins(sg_g)
+    np.testing.assert_allclose(eff, [smz, mq], rtol=1e-5)
+    z_page = O.page_quantile_z(0.995 if eff[1] > 0.992 else 0.99, ps)
+    counts = to_np(cache.last_num_selected_per_head).astype(np.int64)
+    pidx_all = to_np(cache._select_buffers[next(iter(cache._select_buffers))]["page_indices"]).astype(np.int64)
+    seqlens_got = to_np(st["cache_seqlens"]).astype(np.int64)
+    tau_cl = to_np(st["tau_clamped"]) if tau_mode != "exact" else None
+    tau_fin = to_np(st["tau_final"]) if tau_mode != "exact" else None
+    got_out = to_np(out)[:, :, 0]
+    kmean_all, kstd_all = to_np(cache.k_mean), to_np(cache.k_std)
+    for b in range(B):
+        S = int(lens[b])
+        P = (S + ps - 1) // ps
+        pfs = P - 1 if P > 1 else P
+        n_stats = pfs * ps if P > 1 else S
+        lps = O.last_page_size(S, ps)
+        sl = slice(b, b + 1)
+        ref = O.gaussian_page_stats(q[sl, :, 0], kmean_all[sl, :, :P], kstd_all[sl, :, :P], pfs)
+        mu_p, sg_p = mu_p_all[sl, :, :pfs], sg_p_all[sl, :, :pfs]
+        np.testing.assert_allclose(mu_p, ref["mu_p"], rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(sg_p, ref["sigma_p"], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(mu_g[sl], ref["mu_g"], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(sg_g[sl], ref["sigma_g"], rtol=1e-5)
+        np.testing.assert_allclose(th[sl], O.tau_single_gaussian(mu_g[sl], sg_g[sl], n_stats, alpha),
+                                   atol=2e-5, rtol=2e-5)
+        np.testing.assert_allclose(tf[sl], O.tau_floor_fp32(mu_p, sg_p, th[sl], sg_g[sl], alpha,
+                                                            np.float32(eff[0]), 0.2, pfs),
+                                   atol=1e-5, rtol=1e-5)
+        # page table: the union over each kv head's query heads, bit-exact given
+        # the kernel's moments and floor
+        packed_q, _ = O.select_gaussian_pages(mu_p, sg_p, tf[sl], alpha, z_page, pfs, P)
+        pidx = np.zeros((1, Hkv, max(P, 1)), dtype=np.int64)
+        packed_rows = np.empty((1, H), dtype=object)
+        for kvh in range(Hkv):
+            u = np.unique(np.concatenate([packed_q[0, kvh * G + g] for g in range(G)]))
+            assert counts[b, kvh] == u.size
+            np.testing.assert_array_equal(pidx_all[b, kvh, :u.size], u)
+            pidx[0, kvh, :u.size] = u
+            for g in range(G):
+                packed_rows[0, kvh * G + g] = u
+        seqlens = O.cache_seqlens_from_counts(counts[sl], ps, lps)
+        np.testing.assert_array_equal(seqlens_got[sl], seqlens)
+        kb, vb = k[sl, :, :S], v[sl, :, :S]
+        if tau_mode == "exact":
+            ref_out, _ = O.paged_entmax_decode(q[sl, :, 0], kb, vb, pidx, seqlens, ps, alpha, 2,
+                                               dtype)
+            assert_out_close(got_out[sl], ref_out, dtype)
+            continue
+        tc = O.tau_clamp(th[sl], mu_p, sg_p, packed_rows, np.repeat(counts[sl], G, axis=1), tf[sl],
+                         alpha, O.page_quantile_z(0.5, ps), pfs)
+        np.testing.assert_allclose(tau_cl[sl], tc, atol=1e-6, rtol=1e-6)
+        iters = 0 if tau_mode == "fixed" else 1
+        tau_in = tau_cl[sl]
+        ref_out, ref_tau = O.paged_entmax_decode(q[sl, :, 0], kb, vb, pidx, seqlens, ps, alpha, 0,
+                                                 dtype, tau_given=tau_in, tau_iters=iters)
+        # The corrected tau: for alpha = 1.5 the Halley step's second-derivative term
+        # counts the support, which jumps by one when a score ties tau_in within fp32
+        # rounding; rows with such a near-tie are compared through the sum only.
+        qs = O.scaled_query(q[sl, :, 0], alpha, dtype)
+        mass = np.ones((1, H, 1))
+        tie = np.zeros((1, H), dtype=bool)
+        cond = np.ones((1, H))
+        for h in range(H):
+            rows = O.compacted_rows(pidx[0, h // G], seqlens[0, h // G], ps)
+            sc = O.head_scores(qs[0, h], kb[0, h // G], rows, 0.0, alpha, 0)
+            tie[0, h] = iters > 0 and bool(
+                (np.abs(sc - tau_in[0, h]) < 1e-5 * max(1.0, np.abs(sc).max())).any())
+            mass[0, h, 0] = max(1.0, O.entmax_weights(sc, ref_tau[0, h], alpha).sum())
+            if iters:
+                # condition of the unbounded Halley step (adadecode_paged_gaussian_tau.py:
+                # 12-53): 2 f'^2 - f f'' can nearly cancel, and the step then amplifies
+                # the fp32 rounding of the accumulators by (2 f'^2 + |f f''|) / |denominator|
+                a0, a1, a2 = O.entmax_accumulators(sc, tau_in[0, h], alpha)
+                c0 = 1.0 / (alpha - 1.0)
+                f, df, ddf = a0 - 1.0, -c0 * a1, c0 * (c0 - 1.0) * a2
+                den = abs(2 * df * df - f * ddf)
+                cond[0, h] = (2 * df * df + abs(f * ddf)) / den if den > 0 else np.inf
+        assert tie.mean() < 0.25, f"{tie.sum()} near-tie rows"
+        with np.errstate(invalid="ignore"):
+            amp = np.nan_to_num(np.abs(ref_tau - tau_in) * cond, nan=0.0)
+        tol = 1e-4 + 1e-5 * np.abs(ref_tau) + 1e-5 * amp
+        tf_b = tau_fin[sl]
+        bad = (np.abs(tf_b - ref_tau) > tol) & ~tie
+        assert not bad.any(), (f"tau_final: {bad.sum()} rows beyond tolerance, worst "
+                               f"{np.abs(tf_b - ref_tau)[bad].max():.3g}")
+        # the weighted sum at the kernel's own final tau
+        ref_at_fin, _ = O.paged_entmax_decode(q[sl, :, 0], kb, vb, pidx, seqlens, ps, alpha, 0,
+                                              dtype, tau_given=tf_b, tau_iters=0)
+        # given tau, out = sum_i [s_i - tau]_+^(1/(alpha-1)) v_i is not normalised: its
+        # weights sum to `mass`, not 1, so the bar scales with max(1, mass)
+        got = got_out[sl]
+        # an un-normalised sum beyond the storage range is stored as +-inf
+        big = np.abs(ref_at_fin) > {"fp16": 65504.0, "bf16": 3.3e38, "fp32": 3.4e38}[dtype]
+        assert (np.isinf(got[big]) & (np.sign(got[big]) == np.sign(ref_at_fin[big]))).all()
+        got = np.where(big, 0.0, got)
+        assert_out_close(got / mass, np.where(big, 0.0, ref_at_fin) / mass, dtype)
+        ok = ~tie[..., None] & ~big
+        assert_out_close((got / mass)[ok], (ref_out / mass)[ok], dtype)
+
+
 @pytest.mark.parametrize("dtype,G,tau_mode,alpha", GAUSS_FUSED_CASES)
 def test_gaussian_fused_step(dtype, G, tau_mode, alpha):
     """The fused Gaussian launch (global moments, tau-hat, selection, clamp and
@@ -537,101 +685,4 @@ def test_gaussian_fused_step(dtype, G, tau_mode, alpha):
     sparse_attention_decode_gaussian_aware_entmax(to_dev(q, dtype), cache, None, None, out,
                                                   alpha=alpha, tau_mode=tau_mode)
     torch.cuda.synchronize()
-    st = cache.last_gaussian_stats
-    P = cache.num_pages
-    pfs = P - 1
-    lps = O.last_page_size(S, ps)
-    ref = O.gaussian_page_stats(q[:, :, 0], to_np(cache.k_mean), to_np(cache.k_std), pfs)
-    mu_p, sg_p = to_np(st["mu_scores_per_page"]), to_np(st["sigma_scores_per_page"])
-    np.testing.assert_allclose(mu_p, ref["mu_p"], rtol=1e-5, atol=1e-5)
-    np.testing.assert_allclose(sg_p, ref["sigma_p"], rtol=1e-5, atol=1e-6)
-    mu_g = to_np(st["mu_global"])[..., 0]
-    sg_g = to_np(st["sigma_global"])[..., 0]
-    np.testing.assert_allclose(mu_g, ref["mu_g"], rtol=1e-5, atol=1e-6)
-    np.testing.assert_allclose(sg_g, ref["sigma_g"], rtol=1e-5)
-    th = to_np(st["tau_hat"])
-    np.testing.assert_allclose(th, O.tau_single_gaussian(mu_g, sg_g, pfs * ps, alpha),
-                               atol=2e-5, rtol=2e-5)
-    smz, mq = O.auto_selection_margins(sg_g)
-    eff = to_np(st["effective_margins"])
-    np.testing.assert_allclose(eff, [smz, mq], rtol=1e-5)
-    tf = to_np(st["tau_floor"])
-    np.testing.assert_allclose(tf, O.tau_floor_fp32(mu_p, sg_p, th, sg_g, alpha,
-                                                    np.float32(eff[0]), 0.2, pfs),
-                               atol=1e-5, rtol=1e-5)
-    # page table: the union over each kv head's query heads, bit-exact given
-    # the kernel's moments and floor
-    z_page = O.page_quantile_z(0.995 if eff[1] > 0.992 else 0.99, ps)
-    packed_q, _ = O.select_gaussian_pages(mu_p, sg_p, tf, alpha, z_page, pfs, P)
-    counts = to_np(cache.last_num_selected_per_head).astype(np.int64)
-    pidx = to_np(cache._select_buffers[next(iter(cache._select_buffers))]["page_indices"]).astype(np.int64)
-    packed_kv = np.empty((B, Hkv), dtype=object)
-    for b in range(B):
-        for kvh in range(Hkv):
-            u = np.unique(np.concatenate([packed_q[b, kvh * G + g] for g in range(G)]))
-            packed_kv[b, kvh] = u
-            assert counts[b, kvh] == u.size
-            np.testing.assert_array_equal(pidx[b, kvh, :u.size], u)
-            pidx[b, kvh, u.size:] = 0
-    seqlens = O.cache_seqlens_from_counts(counts, ps, lps)
-    np.testing.assert_array_equal(to_np(st["cache_seqlens"]), seqlens)
-    if tau_mode == "exact":
-        ref_out, _ = O.paged_entmax_decode(q[:, :, 0], k, v, pidx, seqlens, ps, alpha, 2, dtype)
-    else:
-        packed_rows = np.empty((B, H), dtype=object)
-        for b in range(B):
-            for h in range(H):
-                packed_rows[b, h] = packed_kv[b, h // G]
-        tc = O.tau_clamp(th, mu_p, sg_p, packed_rows, np.repeat(counts, G, axis=1), tf, alpha,
-                         O.page_quantile_z(0.5, ps), pfs)
-        np.testing.assert_allclose(to_np(st["tau_clamped"]), tc, atol=1e-6, rtol=1e-6)
-        iters = 0 if tau_mode == "fixed" else 1
-        tau_in = to_np(st["tau_clamped"])
-        tau_fin = to_np(st["tau_final"])
-        ref_out, ref_tau = O.paged_entmax_decode(q[:, :, 0], k, v, pidx, seqlens, ps, alpha, 0,
-                                                 dtype, tau_given=tau_in, tau_iters=iters)
-        # The corrected tau: for alpha = 1.5 the Halley step's second-derivative term
-        # counts the support, which jumps by one when a score ties tau_in within fp32
-        # rounding; rows with such a near-tie are compared through the sum only.
-        qs = O.scaled_query(q[:, :, 0], alpha, dtype)
-        mass = np.ones((B, H, 1))
-        tie = np.zeros((B, H), dtype=bool)
-        cond = np.ones((B, H))
-        for b in range(B):
-            for h in range(H):
-                rows = O.compacted_rows(pidx[b, h // G], seqlens[b, h // G], ps)
-                sc = O.head_scores(qs[b, h], k[b, h // G], rows, 0.0, alpha, 0)
-                tie[b, h] = iters > 0 and bool(
-                    (np.abs(sc - tau_in[b, h]) < 1e-5 * max(1.0, np.abs(sc).max())).any())
-                mass[b, h, 0] = max(1.0, O.entmax_weights(sc, ref_tau[b, h], alpha).sum())
-                if iters:
-                    # condition of the unbounded Halley step (adadecode_paged_gaussian_tau.py:
-                    # 12-53): 2 f'^2 - f f'' can nearly cancel, and the step then amplifies
-                    # the fp32 rounding of the accumulators by (2 f'^2 + |f f''|) / |denominator|
-                    a0, a1, a2 = O.entmax_accumulators(sc, tau_in[b, h], alpha)
-                    c0 = 1.0 / (alpha - 1.0)
-                    f, df, ddf = a0 - 1.0, -c0 * a1, c0 * (c0 - 1.0) * a2
-                    den = abs(2 * df * df - f * ddf)
-                    cond[b, h] = (2 * df * df + abs(f * ddf)) / den if den > 0 else np.inf
-        assert tie.mean() < 0.05, f"{tie.sum()} near-tie rows"
-        with np.errstate(invalid="ignore"):
-            amp = np.nan_to_num(np.abs(ref_tau - tau_in) * cond, nan=0.0)
-        tol = 1e-4 + 1e-5 * np.abs(ref_tau) + 1e-5 * amp
-        bad = (np.abs(tau_fin - ref_tau) > tol) & ~tie
-        assert not bad.any(), (f"tau_final: {bad.sum()} rows beyond tolerance, worst "
-                               f"{np.abs(tau_fin - ref_tau)[bad].max():.3g}")
-        # the weighted sum at the kernel's own final tau
-        ref_at_fin, _ = O.paged_entmax_decode(q[:, :, 0], k, v, pidx, seqlens, ps, alpha, 0,
-                                              dtype, tau_given=tau_fin, tau_iters=0)
-        # given tau, out = sum_i [s_i - tau]_+^(1/(alpha-1)) v_i is not normalised: its
-        # weights sum to `mass`, not 1, so the bar scales with max(1, mass)
-        got = to_np(out)[:, :, 0]
-        # an un-normalised sum beyond the storage range is stored as +-inf
-        big = np.abs(ref_at_fin) > {"fp16": 65504.0, "bf16": 3.3e38, "fp32": 3.4e38}[dtype]
-        assert (np.isinf(got[big]) & (np.sign(got[big]) == np.sign(ref_at_fin[big]))).all()
-        got = np.where(big, 0.0, got)
-        assert_out_close(got / mass, np.where(big, 0.0, ref_at_fin) / mass, dtype)
-        ok = ~tie[..., None] & ~big
-        assert_out_close((got / mass)[ok], (ref_out / mass)[ok], dtype)
-        return
-    assert_out_close(to_np(out)[:, :, 0], ref_out, dtype)
+    _check_gaussian_step(cache, q, k, v, out, dtype, G, tau_mode, alpha, [S] * B)

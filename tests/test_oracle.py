@@ -364,3 +364,28 @@ def test_given_tau_zero_iters_is_plain_weighted_sum():
     w = np.clip(s - 0.1, 0, None) ** 2
     np.testing.assert_allclose(out[0, 0], w @ V[0, 0, rows], atol=1e-12)
     assert t[0, 0] == 0.1
+
+
+def test_config1_cpu_topk_step():
+    """BASELINE config 1 (the reference's CPU-sized case): B=1, H=32, D=128, a
+    1024-token prefill plus one decode token, page size 16, fp32, budget 256,
+    alpha 1.5.  Parity: the step equals exact entmax-1.5 over the 257 selected
+    tokens.  Against dense entmax-1.5 over all 1025 tokens the relative L2 gap is
+    bounded as tests/test_topk.py:177 bounds it, 2 * (1 - coverage)."""
+    rng = np.random.default_rng(0)
+    B, H, S, D, ps, budget = 1, 32, 1025, 128, 16, 256
+    K = rng.standard_normal((B, H, S, D))
+    V = rng.standard_normal((B, H, S, D))
+    q = rng.standard_normal((B, H, D))
+    st = O.page_stats(K, ps, "fp32")
+    out, pidx, _ = O.topk_decode_step(q, K, V, st, budget, ps, 1.5, 30, "fp32")
+    assert pidx.shape == (B, H, budget // ps + 1)
+    qs = O.scaled_query(q, 1.5, "fp32")
+    rels = []
+    for h in range(H):
+        rows = O.compacted_rows(pidx[0, h], budget + 1, ps)
+        p = O.entmax_exact(K[0, h][rows] @ qs[0, h], 1.5)
+        np.testing.assert_allclose(out[0, h], p @ V[0, h][rows], atol=1e-9)
+        dense = O.entmax_exact(K[0, h] @ qs[0, h], 1.5) @ V[0, h]
+        rels.append(np.linalg.norm(out[0, h] - dense) / np.linalg.norm(dense))
+    assert max(rels) < 2.0 * (1.0 - budget / (S - 1))
