@@ -53,6 +53,10 @@ def _args():
                         "outlier pages scaled x3 toward q (BASELINE config 3), iid = N(0, 1)")
     p.add_argument("--only", choices=["topk", "gaussian", "criticality"], default=None,
                    help="run one step kind in a loop (for profilers)")
+    p.add_argument("--config", choices=["headline", "c5"], default="headline",
+                   help="c5: BASELINE config 5 instead of the headline line (ragged batch, "
+                        "B=32, 32 q / 8 kv heads, bf16, lengths ~ U[4096, 131072], 1%% outlier "
+                        "pages x4, Gaussian alpha 1.5 with append over 16 consecutive steps)")
     p.add_argument("--copy-calib-mib", type=int, default=0,
                    help="with --only: first copy a buffer of this many MiB (a copy kernel of "
                         "known traffic that scales rocprofv3's FETCH_SIZE / WRITE_SIZE)")
@@ -120,12 +124,100 @@ def _gaussian_cache(B, H, Hkv, L, D, ps, dt, dev, q, kind):
     return cache
 
 
+def _config5(a):
+    """a ragged batch decoded with Gaussian-aware selection.
+
+    B=32, H=32 query / 8 kv heads, D=128, bf16, page size 16; sequence
+    lengths drawn from U[4096, 131072] (seeded, last pages partial); keys and
+    values ~ N(0, 1) with 1% of each (b, kv head)'s pages scaled x4;
+    alpha 1.5, tau_mode "corrected", append_cache=True.  One measurement is
+    16 consecutive decode steps (each appends one token per sequence), after
+    `warmup` untimed steps.  Bytes per step: k_mean + k_std of every
+    statistics page, the selected K and V rows, the appended K/V rows, q and
+    out.
+    """
+    import torch
+
+    from entmaxkv_amd import PagedKVCache, sparse_attention_decode_gaussian_aware_entmax
+
+    B, H, Hkv, D, ps, esz = 32, 32, 8, 128, 16, 2
+    dt, dev = torch.bfloat16, torch.device("cuda:0")
+    g = torch.Generator(device="cpu")
+    g.manual_seed(5)
+    lens = torch.randint(4096, 131072 + 1, (B,), generator=g)
+    Lmax = int(lens.max())
+    gd = torch.Generator(device=dev)
+    gd.manual_seed(5)
+    k = torch.randn(B, Hkv, Lmax, D, device=dev, dtype=dt, generator=gd)
+    P = Lmax // ps
+    n_out = max(1, P // 100)
+    pages = torch.randint(0, P, (B, Hkv, n_out), device=dev, generator=gd)
+    rows = (pages[..., None] * ps + torch.arange(ps, device=dev)).reshape(B, Hkv, -1)
+    kp = torch.gather(k, 2, rows[..., None].expand(-1, -1, -1, D)) * 4.0
+    k.scatter_(2, rows[..., None].expand(-1, -1, -1, D), kp)
+    v = torch.randn(B, Hkv, Lmax, D, device=dev, dtype=dt, generator=gd)
+    cache = PagedKVCache(page_size=ps, headroom=a.warmup + a.steps + 16)
+    cache.initialize(k, v, seq_lens=lens)
+    del k, v, kp
+    torch.cuda.empty_cache()
+    q = torch.randn(B, H, 1, D, device=dev, dtype=dt, generator=gd)
+    kn = torch.randn(B, Hkv, 1, D, device=dev, dtype=dt, generator=gd)
+    vn = torch.randn(B, Hkv, 1, D, device=dev, dtype=dt, generator=gd)
+    out = torch.zeros_like(q)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        sparse_attention_decode_gaussian_aware_entmax(q, cache, kn, vn, out, alpha=1.5,
+                                                      tau_mode="corrected", append_cache=True)
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n_steps = 16
+    sel_tok = 0.0
+    stat_bytes = 0.0
+    t0.record(stream)
+    for _ in range(n_steps):
+        step()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / n_steps
+    # bytes of the last step (lengths grow by one per step: the same to 0.1%)
+    lens_now = cache.seq_lens.long().cpu()
+    Pb = (lens_now + ps - 1) // ps
+    pfs = torch.where(Pb > 1, Pb - 1, Pb)
+    lps = lens_now - (Pb - 1) * ps
+    counts = cache.last_num_selected_per_head.long().cpu()
+    sel_tok = float(((counts - 1).clamp(min=0) * ps + lps[:, None]).sum())
+    stat_bytes = float(pfs.sum()) * Hkv * D * esz * 2
+    step_bytes = stat_bytes + sel_tok * D * esz * 2 + 2 * B * H * D * esz + 2 * B * Hkv * D * esz
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "decode-step us + effective KV GB/s (% HBM peak), BASELINE config 5",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": n_steps,
+        "warmup": a.warmup, "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
+        "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16 storage, f32 accumulate",
+        "data": "synthetic N(0,1) q/k/v with 1% outlier pages x4, seed 5",
+        "config": {"workload": "ragged Gaussian-aware decode, append each step", "batch": B,
+                   "q_heads": H, "kv_heads": Hkv, "head_dim": D, "page_size": ps,
+                   "seq_lens_min": int(lens_now.min()), "seq_lens_max": int(lens_now.max()),
+                   "seq_lens_mean": round(float(lens_now.float().mean()), 1), "alpha": 1.5,
+                   "tau_mode": "corrected", "timing": "eager, 16 consecutive steps",
+                   "mean_selected_pages": round(float(counts.float().mean()), 2),
+                   "bytes_per_step": step_bytes}}), flush=True)
+    return 0
+
+
 def main():
     a = _args()
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
                                    "(multi-GPU sharding is a design note, not built)"}))
         return 2
+    if a.config == "c5":
+        return _config5(a)
     import numpy as np
     import torch
 

@@ -97,14 +97,15 @@ __global__ __launch_bounds__(kThreads) void criticality_kernel(
   const T* kmn = kmin + b * ssb + kvh * ssh;
   const T* kmx = kmax + b * ssb + kvh * ssh;
   const int p_base = blockIdx.x * (SEGS * kUnroll) + seg;
+  if (blockIdx.x * (SEGS * kUnroll) >= num_pages) return;  // past this sequence's pages
+  // unconditional loads (a page past the end re-reads the last one, its
+  // result is discarded) so that all of them are in flight together
   uint4 lo[kUnroll], hi[kUnroll];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int p = p_base + u * SEGS;
-    if (p < num_pages) {
-      lo[u] = ld16(kmn + (int64_t)p * ssp + col);
-      hi[u] = ld16(kmx + (int64_t)p * ssp + col);
-    }
+    const int p = min(p_base + u * SEGS, num_pages - 1);
+    lo[u] = ld16(kmn + (int64_t)p * ssp + col);
+    hi[u] = ld16(kmx + (int64_t)p * ssp + col);
   }
   T* sbase = scores + ((int64_t)b * H + h0) * stride;
 #pragma unroll
@@ -175,7 +176,7 @@ extern "C" int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q
       constexpr int LPR = decltype(lpr)::value;
       return dispatch_group(H / Hkv, [&](auto gv) {
         constexpr int G = decltype(gv)::value;
-        if (B * Hkv >= kHeadPathMinHeads) {
+        if (one_workgroup_per_head(B * Hkv, seq_lens != nullptr)) {
           // one workgroup per (b, kv head), top-k in the same launch
           const int cap = (k_select >= 0 && num_pages <= kMaxStagedKeys) ? num_pages : 0;
           constexpr int U = G >= 8 ? 2 : 16 / G;

@@ -55,7 +55,6 @@ constexpr int kBatch = 8;           // independent loads per lane in score passe
 #define EKV_WAVE_TAU_MAX 4096
 #endif
 constexpr int kWaveTauMax = EKV_WAVE_TAU_MAX;   // longer token lists solve tau with the whole workgroup
-constexpr int kHeadPathMinHeads = 128;
 constexpr int kTablePages = 2048;   // page ids staged in LDS per phase-1 chunk
 
 struct DecodeArgs {

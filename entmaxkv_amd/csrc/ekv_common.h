@@ -356,6 +356,18 @@ __device__ __forceinline__ float fma_rn(float a, float b, float c) { return __fm
 namespace ekv {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// Compute units of the current device (queried once per device).
+int device_cus();
+// The fused one-workgroup-per-(b, kv head) launches win when there are at
+// least half as many heads as compute units: below that, a head's scan spread
+// over many workgroups finishes sooner.  Measured at 128 heads on 256 CUs
+// (BASELINE configs 3 and 4) the fused launches are faster for the top-k step
+// and for Gaussian selections of tens of pages, slower by 30 % for a
+// Gaussian selection of half the cache.  Ragged batches always split: one
+// workgroup per head would wait on the longest sequence.
+inline bool one_workgroup_per_head(int heads, bool ragged) {
+  return !ragged && 2 * heads >= device_cus();
+}
 }  // namespace ekv
 
 namespace ekv {

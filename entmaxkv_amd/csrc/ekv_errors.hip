@@ -1,6 +1,9 @@
-// Error reporting and library metadata for the EntmaxKV C ABI.
+// Error reporting, library metadata and the per-device CU count (the only
+// state the library keeps) for the EntmaxKV C ABI.
 #include <stdarg.h>
 #include <stdio.h>
+
+#include <atomic>
 
 #include "ekv_common.h"
 #include "../../include/entmaxkv.h"
@@ -17,6 +20,20 @@ int set_error(int code, const char* fmt, ...) {
   vsnprintf(g_err, sizeof(g_err), fmt, ap);
   va_end(ap);
   return code;
+}
+
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  cache[dev].store(cus, std::memory_order_relaxed);
+  return cus;
 }
 
 int check_launch(const char* what) {

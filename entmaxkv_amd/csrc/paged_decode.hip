@@ -66,6 +66,13 @@ DecodeArgs make_decode_args(
   return a;
 }
 
+// Workgroups per head of the split scoring launch: about 128 tokens each, at
+// most 256 (the choice of kernels.choose_splits for the same width).
+int splits_for(int max_tokens) {
+  int s = (max_tokens + 127) / 128;
+  return s < 1 ? 1 : (s > 256 ? 256 : s);
+}
+
 }  // namespace
 
 extern "C" int64_t ekv_decode_workspace_bytes(int B, int H, int Hkv, int D, int splits,
@@ -76,7 +83,9 @@ extern "C" int64_t ekv_decode_workspace_bytes(int B, int H, int Hkv, int D, int 
   return ((int64_t)B * H * max_tokens * 4 + 255) / 256 * 256;
 }
 
-extern "C" int ekv_paged_entmax_decode(
+// The decode launch(es); force_split spreads every head over many workgroups
+// (ragged batches, whose heads differ widely in length).
+static int paged_decode(
     const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k, const void* v,
     int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
     const int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h, int n_slots,
@@ -84,7 +93,7 @@ extern "C" int ekv_paged_entmax_decode(
     const int32_t* q_seqlens, const float* alibi_slopes, const float* tau_in, float* tau,
     int tau_mode, int iters, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha,
     float qscale, int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens,
-    void* workspace, int64_t workspace_bytes, int dtype, void* stream) {
+    void* workspace, int64_t workspace_bytes, int dtype, void* stream, bool force_split) {
   EKV_REQUIRE(q && k && v && page_indices && cache_seqlens && tau && out && workspace,
               "ekv_paged_entmax_decode: null pointer");
   EKV_REQUIRE(B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0, "ekv_paged_entmax_decode: bad heads");
@@ -104,7 +113,7 @@ extern "C" int ekv_paged_entmax_decode(
                                   max_tokens, workspace);
   hipStream_t s = (hipStream_t)stream;
   const int G = H / Hkv;
-  const bool head_path = B * Hkv >= kHeadPathMinHeads;
+  const bool head_path = one_workgroup_per_head(B * Hkv, force_split);
   const int cap = kStageBytes / 4 / (G > 0 ? G : 1);
   a.stage_cap = head_path ? (max_tokens < cap ? max_tokens : cap) : 0;
   a.scores_ready = head_path ? 0 : 1;
@@ -114,6 +123,22 @@ extern "C" int ekv_paged_entmax_decode(
       return dec::Launch<T, decltype(gv)::value>::decode(a, B, Hkv, D, head_path, s);
     });
   });
+}
+
+extern "C" int ekv_paged_entmax_decode(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k, const void* v,
+    int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+    const int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h, int n_slots,
+    const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
+    const int32_t* q_seqlens, const float* alibi_slopes, const float* tau_in, float* tau,
+    int tau_mode, int iters, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha,
+    float qscale, int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens,
+    void* workspace, int64_t workspace_bytes, int dtype, void* stream) {
+  return paged_decode(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h, kv_stride_row,
+                      kv_rows, page_indices, pi_stride_b, pi_stride_h, n_slots, cache_seqlens,
+                      cs_stride_b, cs_stride_h, q_seqlens, alibi_slopes, tau_in, tau, tau_mode,
+                      iters, out, out_stride_b, out_stride_h, alpha, qscale, page_size, B, H, Hkv,
+                      D, splits, max_tokens, workspace, workspace_bytes, dtype, stream, false);
 }
 
 extern "C" int ekv_topk_paged_entmax_decode(
@@ -146,16 +171,17 @@ extern "C" int ekv_topk_paged_entmax_decode(
                                   page_size, seq_len, q_pos, k_select, last_page, seq_lens,
                                   page_indices, pi_stride_b, pi_stride_h, dtype, stream);
     if (rc) return rc;
-    return ekv_paged_entmax_decode(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h,
-                                   kv_stride_row, kv_rows, page_indices, pi_stride_b, pi_stride_h,
-                                   n_slots, cache_seqlens, cs_stride_b, cs_stride_h, q_seqlens,
-                                   alibi_slopes, nullptr, tau, 0, niter, out, out_stride_b,
-                                   out_stride_h, alpha, qscale, page_size, B, H, Hkv, D, splits,
-                                   max_tokens, workspace, workspace_bytes, dtype, stream);
+    return paged_decode(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h, kv_stride_row,
+                        kv_rows, page_indices, pi_stride_b, pi_stride_h, n_slots, cache_seqlens,
+                        cs_stride_b, cs_stride_h, q_seqlens, alibi_slopes, nullptr, tau, 0, niter,
+                        out, out_stride_b, out_stride_h, alpha, qscale, page_size, B, H, Hkv, D,
+                        splits, max_tokens, workspace, workspace_bytes, dtype, stream,
+                        seq_lens != nullptr);
   };
   // one launch when every head fills a workgroup and its keys, page table and
   // scores stay in LDS; otherwise criticality+top-k, then the decode
-  if (B * Hkv < kHeadPathMinHeads || num_pages > topk::kMaxStagedKeys || n_slots > kTablePages)
+  if (!one_workgroup_per_head(B * Hkv, seq_lens != nullptr) || num_pages > topk::kMaxStagedKeys ||
+      n_slots > kTablePages)
     return two_launches();
   const int tokens = max_tokens < n_slots * page_size ? max_tokens : n_slots * page_size;
   DecodeArgs a = make_decode_args(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h,
@@ -229,7 +255,7 @@ extern "C" int ekv_gaussian_paged_entmax_decode(
   hipStream_t s = (hipStream_t)stream;
   const int G = H / Hkv;
   const float* tau_start = tau_clamped ? tau_clamped : tau_hat;
-  if (B * Hkv < kHeadPathMinHeads) {
+  if (!one_workgroup_per_head(B * Hkv, seq_lens != nullptr)) {
     // few heads: moments, selection and a split decode as separate launches
     int rc = gauss::launch_finalize(moments_workspace, B, H, Hkv, pages_for_stats, mu_g, sigma_g,
                                     mean_var, var_means, tau_hat_given ? nullptr : tau_hat, alpha,
@@ -242,12 +268,12 @@ extern "C" int ekv_gaussian_paged_entmax_decode(
                                   cache_seqlens, page_size, last_page_size, tau_clamped, z_clamp,
                                   eps, effective_margins, seq_lens, stream);
     if (rc) return rc;
-    return ekv_paged_entmax_decode(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h,
-                                   kv_stride_row, kv_rows, page_indices, pi_stride_b, pi_stride_h,
-                                   num_pages, cache_seqlens, Hkv, 1, q_seqlens, alibi_slopes,
-                                   tau_start, tau, tau_mode, iters, out, out_stride_b,
-                                   out_stride_h, alpha, qscale, page_size, B, H, Hkv, D, 1,
-                                   max_tokens, workspace, workspace_bytes, dtype, stream);
+    return paged_decode(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h, kv_stride_row,
+                        kv_rows, page_indices, pi_stride_b, pi_stride_h, num_pages, cache_seqlens,
+                        Hkv, 1, q_seqlens, alibi_slopes, tau_start, tau, tau_mode, iters, out,
+                        out_stride_b, out_stride_h, alpha, qscale, page_size, B, H, Hkv, D,
+                        splits_for(max_tokens), max_tokens, workspace, workspace_bytes, dtype,
+                        stream, seq_lens != nullptr);
   }
   DecodeArgs a = make_decode_args(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h,
                                   kv_stride_row, kv_rows, page_indices, pi_stride_b, pi_stride_h,

@@ -19,8 +19,6 @@ constexpr int kUnroll = 4;  // pages per segment per workgroup
 // Page keys staged in LDS by the top-k pass (16384 pages = 256k tokens at
 // page size 16, 64 KB); longer caches re-read the scores on every pass.
 constexpr int kMaxStagedKeys = 16384;
-// Batch * kv heads from which one workgroup per head fills the GPU.
-constexpr int kHeadPathMinHeads = 128;
 
 // Top-k geometry of batch element b.  With per-sequence lengths, sequence b
 // scores its pages [0, P_b - 1) (the partial last page excluded), selects
