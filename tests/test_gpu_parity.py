@@ -553,12 +553,15 @@ GAUSS_FUSED_CASES = [("fp16", 1, "corrected", 1.5), ("bf16", 1, "exact", 1.5),
                      ("bf16", 2, "corrected", 2.0), ("fp16", 8, "exact", 1.5)]
 
 
-def _check_gaussian_step(cache, q, k, v, out, dtype, G, tau_mode, alpha, lens):
+def _check_gaussian_step(cache, q, k, v, out, dtype, G, tau_mode, alpha, lens, slopes=None):
     """The Gaussian step's stages against the oracle, sequence by sequence.
 
     ``lens`` [B]: the sequence lengths (all equal for a uniform batch).  The
     automatic margins are batch-wide, so they come from every head's sigma_g;
-    everything else is per sequence."""
+    everything else is per sequence.  With ALiBi ``slopes`` [H] the page means
+    carry the page-mean bias, tau-hat is the page-mixture root and the decode
+    adds the position bias at q position lens[b] - 1 (the step is run with
+    q_seqlens = lens)."""
     st = cache.last_gaussian_stats
     ps = cache.page_size
     B, H = q.shape[:2]
@@ -588,12 +591,18 @@ def _check_gaussian_step(cache, q, k, v, out, dtype, G, tau_mode, alpha, lens):
         sl = slice(b, b + 1)
         ref = O.gaussian_page_stats(q[sl, :, 0], kmean_all[sl, :, :P], kstd_all[sl, :, :P], pfs)
         mu_p, sg_p = mu_p_all[sl, :, :pfs], sg_p_all[sl, :, :pfs]
-        np.testing.assert_allclose(mu_p, ref["mu_p"], rtol=1e-5, atol=1e-5)
+        ref_mu = ref["mu_p"]
+        if slopes is not None:
+            ref_mu = ref_mu + O.alibi_page_mean_bias(slopes, pfs, S, ps)[None]
+        np.testing.assert_allclose(mu_p, ref_mu, rtol=1e-5, atol=1e-5)
         np.testing.assert_allclose(sg_p, ref["sigma_p"], rtol=1e-5, atol=1e-6)
         np.testing.assert_allclose(mu_g[sl], ref["mu_g"], rtol=1e-5, atol=1e-6)
         np.testing.assert_allclose(sg_g[sl], ref["sigma_g"], rtol=1e-5)
-        np.testing.assert_allclose(th[sl], O.tau_single_gaussian(mu_g[sl], sg_g[sl], n_stats, alpha),
-                                   atol=2e-5, rtol=2e-5)
+        if slopes is None:
+            ref_th = O.tau_single_gaussian(mu_g[sl], sg_g[sl], n_stats, alpha)
+        else:
+            ref_th = O.tau_page_mixture(mu_p, sg_p, float(ps), alpha)
+        np.testing.assert_allclose(th[sl], ref_th, atol=5e-5, rtol=2e-5)
         np.testing.assert_allclose(tf[sl], O.tau_floor_fp32(mu_p, sg_p, th[sl], sg_g[sl], alpha,
                                                             np.float32(eff[0]), 0.2, pfs),
                                    atol=1e-5, rtol=1e-5)
@@ -612,18 +621,19 @@ def _check_gaussian_step(cache, q, k, v, out, dtype, G, tau_mode, alpha, lens):
         seqlens = O.cache_seqlens_from_counts(counts[sl], ps, lps)
         np.testing.assert_array_equal(seqlens_got[sl], seqlens)
         kb, vb = k[sl, :, :S], v[sl, :, :S]
+        ali = {} if slopes is None else {"alibi_slopes": slopes, "q_seqlens": np.array([S])}
         if tau_mode == "exact":
             ref_out, _ = O.paged_entmax_decode(q[sl, :, 0], kb, vb, pidx, seqlens, ps, alpha, 2,
-                                               dtype)
+                                               dtype, **ali)
             assert_out_close(got_out[sl], ref_out, dtype)
             continue
         tc = O.tau_clamp(th[sl], mu_p, sg_p, packed_rows, np.repeat(counts[sl], G, axis=1), tf[sl],
                          alpha, O.page_quantile_z(0.5, ps), pfs)
         np.testing.assert_allclose(tau_cl[sl], tc, atol=1e-6, rtol=1e-6)
-        iters = 0 if tau_mode == "fixed" else 1
+        iters = 0 if tau_mode == "fixed" else (1 if slopes is None else 2)
         tau_in = tau_cl[sl]
         ref_out, ref_tau = O.paged_entmax_decode(q[sl, :, 0], kb, vb, pidx, seqlens, ps, alpha, 0,
-                                                 dtype, tau_given=tau_in, tau_iters=iters)
+                                                 dtype, tau_given=tau_in, tau_iters=iters, **ali)
         # The corrected tau: for alpha = 1.5 the Halley step's second-derivative term
         # counts the support, which jumps by one when a score ties tau_in within fp32
         # rounding; rows with such a near-tie are compared through the sum only.
@@ -633,7 +643,8 @@ def _check_gaussian_step(cache, q, k, v, out, dtype, G, tau_mode, alpha, lens):
         cond = np.ones((1, H))
         for h in range(H):
             rows = O.compacted_rows(pidx[0, h // G], seqlens[0, h // G], ps)
-            sc = O.head_scores(qs[0, h], kb[0, h // G], rows, 0.0, alpha, 0)
+            sc = O.head_scores(qs[0, h], kb[0, h // G], rows,
+                               0.0 if slopes is None else float(slopes[h]), alpha, S - 1)
             tie[0, h] = iters > 0 and bool(
                 (np.abs(sc - tau_in[0, h]) < 1e-5 * max(1.0, np.abs(sc).max())).any())
             mass[0, h, 0] = max(1.0, O.entmax_weights(sc, ref_tau[0, h], alpha).sum())
@@ -656,7 +667,7 @@ def _check_gaussian_step(cache, q, k, v, out, dtype, G, tau_mode, alpha, lens):
                                f"{np.abs(tf_b - ref_tau)[bad].max():.3g}")
         # the weighted sum at the kernel's own final tau
         ref_at_fin, _ = O.paged_entmax_decode(q[sl, :, 0], kb, vb, pidx, seqlens, ps, alpha, 0,
-                                              dtype, tau_given=tf_b, tau_iters=0)
+                                              dtype, tau_given=tf_b, tau_iters=0, **ali)
         # given tau, out = sum_i [s_i - tau]_+^(1/(alpha-1)) v_i is not normalised: its
         # weights sum to `mass`, not 1, so the bar scales with max(1, mass)
         got = got_out[sl]
@@ -686,3 +697,30 @@ def test_gaussian_fused_step(dtype, G, tau_mode, alpha):
                                                   alpha=alpha, tau_mode=tau_mode)
     torch.cuda.synchronize()
     _check_gaussian_step(cache, q, k, v, out, dtype, G, tau_mode, alpha, [S] * B)
+
+
+@pytest.mark.parametrize("path", ["head", "split"])
+def test_gaussian_alibi_step(path):
+    """ALiBi through the Gaussian step: page-mean bias on the page means,
+    page-mixture tau-hat given to the fused launch, two corrections and the
+    position bias in the decode (attention_gaussian.py:103-140,
+    gaussian_utils.py:142-181)."""
+    from entmaxkv_amd import PagedKVCache, sparse_attention_decode_gaussian_aware_entmax
+    _case(test="gaussian_alibi", path=path)
+    dtype, alpha, G = "fp16", 1.5, 2
+    rng = np.random.default_rng(91)
+    B, Hkv = (8, 16) if path == "head" else (2, 2)
+    S, D, ps = 16 * 64 + 7, 64, 16
+    H = Hkv * G
+    q, k, v = _gqa_gaussian_inputs(rng, dtype, B, Hkv, G, S, D, 0.03)
+    slopes = np.exp2(-8.0 * np.arange(1, H + 1) / H).astype(np.float32)
+    cache = PagedKVCache(page_size=ps)
+    cache.initialize(to_dev(k, dtype), to_dev(v, dtype))
+    out = torch.zeros(B, H, 1, D, dtype=TORCH_DT[dtype], device="cuda")
+    sparse_attention_decode_gaussian_aware_entmax(
+        to_dev(q, dtype), cache, None, None, out, alpha=alpha, tau_mode="corrected",
+        alibi_slopes=torch.tensor(slopes, device="cuda"),
+        q_seqlens=torch.full((B,), S, dtype=torch.int32, device="cuda"))
+    torch.cuda.synchronize()
+    _check_gaussian_step(cache, q, k, v, out, dtype, G, "corrected", alpha, [S] * B,
+                         slopes=slopes.astype(np.float64))
