@@ -447,6 +447,7 @@ __device__ __forceinline__ float solve_tau(S& sp, const DecodeArgs& a, const flo
       }
     }
     const float gmax = sp.max(m);
+    EKV_STAMP(7);
     const float t0 = gmax - 1.0f;
     for (int b0 = 0; b0 < n; b0 += S::kStride * kBatch) {
 #pragma unroll

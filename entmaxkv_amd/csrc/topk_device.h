@@ -78,6 +78,22 @@ template <> struct ScoreKey<float> {
   }
 };
 
+// Adds one to hist[bin] for every active lane of the wave; lanes that share a
+// bin add together with one LDS atomic (the top digit of the page scores falls
+// into a handful of bins, and same-address atomics serialise).  The loop runs
+// once per distinct bin among the active lanes.
+__device__ __forceinline__ void wave_hist_add(unsigned* hist, uint32_t bin, bool act) {
+  uint64_t m = __ballot(act);
+  while (m) {
+    const int leader = (int)__builtin_ctzll(m);
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)bin, leader);
+    const uint64_t same = __ballot(act && bin == b);
+    if ((int)(threadIdx.x & 63) == leader) atomicAdd(&hist[b], (unsigned)__popcll(same));
+    m &= ~same;
+    if (bin == b) act = false;
+  }
+}
+
 // Block-wide top-k over `num_pages` group keys; writes ascending indices to
 // out[0..k) (and lds_out[0..k) when non-null) and `last_page` to out[k] when
 // last_page >= 0.  blockDim == NT.  The keys come from `lds_keys` when
@@ -154,8 +170,14 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
           const int p = p0 + j * NT + tid;
-          if (p < num_pages && (kv[j] & pmask) == prefix)
-            atomicAdd(&hist[pass][(kv[j] >> shift) & 255u], 1u);
+          const bool act = p < num_pages && (kv[j] & pmask) == prefix;
+          const uint32_t bin = (kv[j] >> shift) & 255u;
+          if (pass == 0) {
+            // wave-uniform: every lane takes part in the ballots
+            if (p0 + j * NT < num_pages) wave_hist_add(hist[0], bin, act);
+          } else if (act) {
+            atomicAdd(&hist[pass][bin], 1u);
+          }
         }
       }
       __syncthreads();
