@@ -27,9 +27,9 @@
 // Experiment builds only (-DEKV_PHASE_TIMERS on one decode_inst unit):
 // per-workgroup wall-clock stamps (100 MHz) of the fused kernels' phases.
 #ifdef EKV_PHASE_TIMERS
-__device__ unsigned long long ekv_phase_timers[4096 * 8];
+__device__ unsigned long long ekv_phase_timers[4096 * 16];
 #define EKV_STAMP(i) \
-  if (threadIdx.x == 0 && blockIdx.x < 4096) ekv_phase_timers[blockIdx.x * 8 + (i)] = wall_clock64()
+  if (threadIdx.x == 0 && blockIdx.x < 4096) ekv_phase_timers[blockIdx.x * 16 + (i)] = wall_clock64()
 // slot 6 in the top-k launch: the top-k threshold found (topk_device.h stamp 3)
 #define EKV_CSTAMP(i) \
   if ((i) == 3) EKV_STAMP(6)
@@ -460,12 +460,15 @@ __device__ __forceinline__ float solve_tau(S& sp, const DecodeArgs& a, const flo
       }
     }
     sp.sync();
+    EKV_STAMP(8);
     float t_lo, t_hi;
     histogram_init(hist, gmax, alpha, t, t_lo, t_hi);
+    EKV_STAMP(9);
     for (int it = 0; it < a.iters; ++it) {
       float a0, a1, a2;
       accumulate_pass(sp, sc, n, t, alpha, c0, a0, a1, a2);
       halley_bisect(t, t_lo, t_hi, a0, a1, a2, c0, c1);
+      if (it < 2) EKV_STAMP(10 + it);
     }
   } else {
     t = tau_in;
@@ -628,21 +631,23 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
       for (int g = 0; g < G; ++g) sh.sup_p[g * kHeadThreads + slot] = p[g];
     }
     __syncthreads();
-    // four support rows per segment in flight (a slot past nsup re-reads the
-    // last row and is not accumulated)
-    for (int j0 = seg; j0 < nsup; j0 += 4 * SEGS) {
-      Vec<T> x[4];
+    // eight support rows per segment in flight, kept raw until converted (a
+    // slot past nsup re-reads the last row and is not accumulated)
+    constexpr int R = 8;
+    for (int j0 = seg; j0 < nsup; j0 += R * SEGS) {
+      uint4 x[R];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) x[r].load(vh + sh.sup_row[min(j0 + r * SEGS, nsup - 1)] * a.ksr + col);
+      for (int r = 0; r < R; ++r) x[r] = ld16(vh + sh.sup_row[min(j0 + r * SEGS, nsup - 1)] * a.ksr + col);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int r = 0; r < R; ++r) {
         const int j = j0 + r * SEGS;
         if (j < nsup) {
+          const T* e = reinterpret_cast<const T*>(&x[r]);
 #pragma unroll
           for (int g = 0; g < G; ++g) {
             const float w = sh.sup_p[g * kHeadThreads + j];
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) acc[g][i] += w * x[r].v[i];
+            for (int i = 0; i < VEC; ++i) acc[g][i] += w * to_f<T>(e[i]);
           }
         }
       }
@@ -793,6 +798,7 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
   __shared__ int s_pages[kTablePages];
   __shared__ float s_th[G], s_sg[G], s_tin[G];
   __shared__ float scratch[kWaves];
+  __shared__ float ups[G][kWaves];
   HeadShared sh{hist, part, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
   sh.tau_in_lds = s_tin;
 
@@ -810,6 +816,10 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
   const int s2 = gauss::split_lanes(f.splits);
   const int own0 = b * a.H + kvh * G;
   const int lane = tid & 63;
+  // this sequence's statistics pages (ragged batch) within rows of stride sel.pages
+  const int own_pages = sel.seq_lens
+                            ? min(seq_pages(sel.seq_lens[b], sel.page_size).stat_pages, sel.pages)
+                            : sel.pages;
   if (wid < G) {
     const int h = own0 + wid;
     float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -837,24 +847,36 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
       f.var_means[h] = m.var_means;
       if (!f.tau_hat_given) f.tau_hat[h] = th;
     }
-  } else if (sel.auto_margins) {
+  } else {
     const int nt = (kWaves - G) * 64, t = tid - G * 64;
-    const int hpp = nt / s2;  // heads per pass
-    float ssum = 0.f;
-    for (int base = 0; base < nh; base += hpp) {
-      const int h = base + t / s2, j = t % s2;
-      const bool ok = t < hpp * s2 && h < nh;
-      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (ok && j < f.splits) x = f.partials[(int64_t)h * f.splits + j];
-      x = gauss::reduce_splits(x, s2);
-      if (ok && j == 0) {
-        const int hp = sel.seq_lens ? seq_pages(sel.seq_lens[h / a.H], sel.page_size).stat_pages
-                                    : sel.pages;
-        ssum += gauss::finalize_moments(x, hp).sigma_g;
+    if (sel.auto_margins) {
+      const int hpp = nt / s2;  // heads per pass
+      float ssum = 0.f;
+      for (int base = 0; base < nh; base += hpp) {
+        const int h = base + t / s2, j = t % s2;
+        const bool ok = t < hpp * s2 && h < nh;
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (ok && j < f.splits) x = f.partials[(int64_t)h * f.splits + j];
+        x = gauss::reduce_splits(x, s2);
+        if (ok && j == 0) {
+          const int hp = sel.seq_lens ? seq_pages(sel.seq_lens[h / a.H], sel.page_size).stat_pages
+                                      : sel.pages;
+          ssum += gauss::finalize_moments(x, hp).sigma_g;
+        }
       }
+      ssum = wave_sum(ssum);
+      if (lane == 0) scratch[wid] = ssum;
     }
-    ssum = wave_sum(ssum);
-    if (lane == 0) scratch[wid] = ssum;
+    // the selection's mean of mu_p + 1.5 sigma_p per head (independent of tau-hat)
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t row = ((int64_t)b * a.H + kvh * G + g) * sel.pages;
+      float u = 0.f;
+      for (int p = t; p < own_pages; p += nt)
+        u += fma_rn(1.5f, sel.sigma_p[row + p], sel.mu_p[row + p]);
+      u = wave_sum(u);
+      if (lane == 0) ups[g][wid] = u;
+    }
   }
   __syncthreads();
   float sbar = 0.f;
@@ -862,10 +884,19 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
     for (int w = G; w < kWaves; ++w) sbar += scratch[w];
     sbar /= (float)nh;
   }
+  // every thread forms the means itself (same order, same bits): no second barrier
+  float upper[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float u = 0.f;
+    for (int w = G; w < kWaves; ++w) u += ups[g][w];
+    upper[g] = u / (float)own_pages;
+  }
   EKV_STAMP(6);
   EKV_STAMP(1);
   const int count = gauss::select_pack_block<G, kHeadThreads>(sel, b, kvh, sbar, s_th, s_sg,
-                                                              s_pages, kTablePages, s_tin);
+                                                              s_pages, kTablePages, s_tin,
+                                                              upper);
   __syncthreads();
   EKV_STAMP(2);
 

@@ -224,7 +224,10 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int h0 = kvh * G;
 
-  float qs[G][VEC], qq[G][VEC];
+  // qs = q / sqrt(D); the variance term is accumulated as (std_d |qs_d|)^2,
+  // two operations per element (the product is rounded once more than
+  // std_d^2 * qs_d^2, a relative change of 2^-24 per term)
+  float qs[G][VEC], qa[G][VEC];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     Vec<T> x;
@@ -232,7 +235,7 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
       qs[g][i] = x.v[i] * a.scale;
-      qq[g][i] = qs[g][i] * qs[g][i];
+      qa[g][i] = fabsf(qs[g][i]);
     }
   }
   const T* km = (const T*)a.kmean + b * a.ssb + kvh * a.ssh;
@@ -272,9 +275,9 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
         float mu = 0.f, var = 0.f;
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          const float sd = sv[u].get(i);
+          const float w = sv[u].get(i) * qa[g][i];
           mu += mv[u].get(i) * qs[g][i];
-          var += (sd * sd) * qq[g][i];
+          var += w * w;
         }
         mu = seg_sum<LPR>(mu);
         var = seg_sum<LPR>(var);
@@ -420,16 +423,24 @@ __device__ __forceinline__ TauGeom tau_geom(const int32_t* seq_lens, int b, int 
 // (+ the last page as sentinel) to global memory and, for slots < lds_cap, to
 // `lds_pages`; the count, tau floor, compacted length and (with clamp) the
 // clamped tau, which is also returned in tau_out[g] (tau-hat when not
-// clamping).  Returns the page count.  blockDim == NT; every thread returns
-// the same count.
+// clamping).  `upper_in[g]`, when given, is the head's mean of
+// mu_p + 1.5 sigma_p over the pages (else computed here).  Returns the page
+// count.  blockDim == NT; every thread returns the same count.
+//
+// Pack: each wave owns a contiguous range of pages; one pass counts its
+// selected pages (ballots), one barrier publishes the counts, a second pass
+// writes them at their ranks.  Selected page ids therefore come out ascending.
 template <int G, int NT>
 __device__ __forceinline__ int select_pack_block(const SelectArgs& a, int b, int kvh, float sbar,
                                                  const float* tau_hat, const float* sig_g,
-                                                 int* lds_pages, int lds_cap, float* tau_out) {
+                                                 int* lds_pages, int lds_cap, float* tau_out,
+                                                 const float* upper_in = nullptr) {
+  constexpr int W = NT / 64;
   __shared__ float scratch[16];
-  __shared__ int scan_scratch[NT / 64 + 1];
-  __shared__ float cm[NT / 64];
+  __shared__ int wave_cnt[W];
+  __shared__ float cm[G][W];
   const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
   const int bkv = b * a.Hkv + kvh;
   const int h0 = kvh * G;
   // this sequence's pages (ragged batch) within rows of stride a.pages
@@ -460,9 +471,14 @@ __device__ __forceinline__ int select_pack_block(const SelectArgs& a, int b, int
     const int h = h0 + g;
     mu[g] = a.mu_p + ((int64_t)b * a.H + h) * a.pages;
     sg[g] = a.sigma_p + ((int64_t)b * a.H + h) * a.pages;
-    float s = 0.f;
-    for (int p = tid; p < pages; p += NT) s += fma_rn(1.5f, sg[g][p], mu[g][p]);
-    const float upper = block_sum(s, scratch) / (float)pages;
+    float upper;
+    if (upper_in) {
+      upper = upper_in[g];
+    } else {
+      float s = 0.f;
+      for (int p = tid; p < pages; p += NT) s += fma_rn(1.5f, sg[g][p], mu[g][p]);
+      upper = block_sum(s, scratch) / (float)pages;
+    }
     const float th = tau_hat[g];
     const float thr = th / a.am1;
     const float sig_delta = smz * sig_g[g];
@@ -473,44 +489,65 @@ __device__ __forceinline__ int select_pack_block(const SelectArgs& a, int b, int
     if (tid == 0) a.tau_floor[b * a.H + h] = tfloor[g];
   }
 
+  // page p is selected when any query head of the group selects it
+  auto selected = [&](int p) {
+    bool sel = false;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      if (mul_rn(a.am1, fma_rn(z_page, sg[g][p], mu[g][p])) > tfloor[g]) sel = true;
+    return sel;
+  };
   const float third = 0.3333333333333333f;
   float capmax[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) capmax[g] = -INFINITY;
-  int32_t* out = a.page_indices + b * a.pisb + kvh * a.pish;
-  int base = 0;
-  for (int c0 = 0; c0 < pages; c0 += NT) {
-    const int p = c0 + tid;
-    bool sel = false;
-    if (p < pages) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float m = mu[g][p], s = sg[g][p];
-        if (mul_rn(a.am1, fma_rn(z_page, s, m)) > tfloor[g]) sel = true;
-      }
-      if (sel) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float cap = fma_rn(mul_rn(a.z_clamp, sg[g][p]), third, mu[g][p]);
-          capmax[g] = fmaxf(capmax[g], cap);
-        }
-      }
-    }
-    int tot;
-    const int pos = block_excl_scan(sel ? 1 : 0, scan_scratch, &tot);
+  const int per = (pages + W - 1) / W;
+  const int pw0 = min(pages, wid * per), pw1 = min(pages, pw0 + per);
+  int cnt = 0;
+  for (int r0 = pw0; r0 < pw1; r0 += 64) {
+    const int p = r0 + lane;
+    const bool sel = p < pw1 && selected(p);
     if (sel) {
-      out[base + pos] = p;
-      if (base + pos < lds_cap) lds_pages[base + pos] = p;
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        capmax[g] = fmaxf(capmax[g], fma_rn(mul_rn(a.z_clamp, sg[g][p]), third, mu[g][p]));
     }
-    base += tot;
+    cnt += __popcll(__ballot(sel));
   }
-  int count = base;
+  if (lane == 0) wave_cnt[wid] = cnt;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float m = wave_max(capmax[g]);
+    if (lane == 0) cm[g][wid] = m;
+  }
+  __syncthreads();
+  int base = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    const int c = wave_cnt[w];
+    base += w < wid ? c : 0;
+    total += c;
+  }
+  int32_t* out = a.page_indices + b * a.pisb + kvh * a.pish;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  for (int r0 = pw0; r0 < pw1; r0 += 64) {
+    const int p = r0 + lane;
+    const bool sel = p < pw1 && selected(p);
+    const uint64_t m = __ballot(sel);
+    if (sel) {
+      const int slot = base + __popcll(m & below);
+      out[slot] = p;
+      if (slot < lds_cap) lds_pages[slot] = p;
+    }
+    base += __popcll(m);
+  }
+  int count = total;
   if (num_pages > pages) {
     if (tid == 0) {
-      out[base] = num_pages - 1;
-      if (base < lds_cap) lds_pages[base] = num_pages - 1;
+      out[total] = num_pages - 1;
+      if (total < lds_cap) lds_pages[total] = num_pages - 1;
     }
-    count = base + 1;
+    count = total + 1;
   }
   if (tid == 0) {
     a.counts[bkv] = count;
@@ -519,22 +556,17 @@ __device__ __forceinline__ int select_pack_block(const SelectArgs& a, int b, int
   // clamp: tau = min(tau_hat, max((alpha-1) * max cap over the selection - eps, floor))
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    if (a.tau_clamped) {
-      const float m = wave_max(capmax[g]);
-      if ((tid & 63) == 0) cm[tid >> 6] = m;
-      __syncthreads();
-      if (tid == 0) {
+    if (tid == g) {
+      const float th = tau_hat[g];
+      float tc = th;
+      if (a.tau_clamped) {
         float mx = -INFINITY;
-        for (int w = 0; w < NT / 64; ++w) mx = fmaxf(mx, cm[w]);
-        const float th = tau_hat[g];
+        for (int w = 0; w < W; ++w) mx = fmaxf(mx, cm[g][w]);
         const float up = fmaxf(fma_rn(a.am1, mx, -a.eps), tfloor[g]);
-        const float tc = (mx > -3.0e38f) ? fminf(th, up) : th;
+        tc = (mx > -3.0e38f) ? fminf(th, up) : th;
         a.tau_clamped[b * a.H + h0 + g] = tc;
-        if (tau_out) tau_out[g] = tc;
       }
-      __syncthreads();
-    } else if (tid == 0 && tau_out) {
-      tau_out[g] = tau_hat[g];
+      if (tau_out) tau_out[g] = tc;
     }
   }
   return count;
