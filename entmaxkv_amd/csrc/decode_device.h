@@ -136,7 +136,7 @@ __device__ __forceinline__ void load_query(const DecodeArgs& a, int b, int h0, i
 template <typename T, int LPR, int G, int NT, int U, typename PagePtr>
 __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, int c_begin,
                                            int c_end, float* sc, int64_t stride, PagePtr pages,
-                                           int c_base) {
+                                           int c_base, float* run_max = nullptr) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int SEGS = NT / LPR;
   constexpr int ROWS = SEGS * U;
@@ -180,11 +180,12 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
       for (int g = 0; g < G; ++g) {
         float acc = Dot16<T>::dot(qraw[g], kv[u], 0.f);
         acc = seg_sum<LPR>(acc);
-        if (c < c_end && sl == 0) {
+        if (c < c_end) {
           float s = acc;
           if (rows[u] < 0) s = -INFINITY;
           else if (a.slopes) s += slope[g] * (float)(rows[u] - q_idx);
-          sc[g * stride + c] = s;
+          if (sl == 0) sc[g * stride + c] = s;
+          if (run_max) run_max[g] = fmaxf(run_max[g], s);
         }
       }
     }
@@ -432,21 +433,24 @@ __device__ __forceinline__ void accumulate_pass(S& sp, const float* __restrict__
 // must be zero on entry when tau_mode is 0.
 template <typename S>
 __device__ __forceinline__ float solve_tau(S& sp, const DecodeArgs& a, const float* __restrict__ sc,
-                                           int n, float tau_in, int* hist) {
+                                           int n, float tau_in, int* hist, const float* pre_max) {
   const float alpha = a.alpha;
   const float c0 = 1.0f / (alpha - 1.0f);
   const float c1 = c0 - 1.0f;
   float t;
   if (a.tau_mode == 0) {
     float m = -1.0e6f;
-    for (int b0 = 0; b0 < n; b0 += S::kStride * kBatch) {
+    // the max of the scores, from the scoring phase when it ran in this launch
+    if (pre_max) {
+      m = *pre_max;
+    } else for (int b0 = 0; b0 < n; b0 += S::kStride * kBatch) {
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
         const int c = b0 + j * S::kStride + sp.first();
         if (c < n) m = fmaxf(m, sc[c]);
       }
     }
-    const float gmax = sp.max(m);
+    const float gmax = pre_max ? m : sp.max(m);
     EKV_STAMP(7);
     const float t0 = gmax - 1.0f;
     for (int b0 = 0; b0 < n; b0 += S::kStride * kBatch) {
@@ -515,6 +519,7 @@ struct HeadShared {
   float* red;    // [kWaves][D]
   int* s_pages;  // [kTablePages]
   const float* tau_in_lds = nullptr;  // [G] starting tau in LDS (else a.tau_in)
+  float* wmax = nullptr;              // [G][kWaves] per-wave score maxima of phase 1
 };
 
 // tau of the G heads of one (b, kv head): head g is solved by the team of W
@@ -530,7 +535,13 @@ __device__ __forceinline__ void solve_heads(const DecodeArgs& a, int b, int h0, 
   const bool real = g < G;
   float tin = 0.f;
   if (real && a.tau_mode == 1) tin = sh.tau_in_lds ? sh.tau_in_lds[g] : a.tau_in[b * a.H + h0 + g];
-  const float t = solve_tau(sp, a, sc + (real ? g : 0) * stride, real ? n : 0, tin, sh.hist[g]);
+  // every team takes the same path (the reductions of a team of W > 1 waves
+  // are workgroup barriers)
+  float pm = -1.0e6f;
+  if (sh.wmax && real)
+    for (int w = 0; w < kWaves; ++w) pm = fmaxf(pm, sh.wmax[g * kWaves + w]);
+  const float t = solve_tau(sp, a, sc + (real ? g : 0) * stride, real ? n : 0, tin, sh.hist[g],
+                            sh.wmax ? &pm : nullptr);
   if (real && sp.pos == 0 && sp.lane == 0) sh.s_tau[g] = t;
 }
 
@@ -538,8 +549,12 @@ __device__ __forceinline__ void solve_heads(const DecodeArgs& a, int b, int h0, 
 // score access is a ds_* instruction) and to the workspace otherwise.
 template <typename T, int LPR, int G, int U, bool kStaged, bool kTableInLds = false>
 __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int kvh, int n,
-                                                 float* sc, int64_t stride, const HeadShared& sh,
+                                                 float* sc, int64_t stride,
+                                                 const HeadShared& sh_in,
                                                  bool first_chunk_staged = false) {
+  // the per-wave maxima reach the tau solve only when phase 1 runs here
+  HeadShared sh = sh_in;
+  if (a.scores_ready && !kTableInLds) sh.wmax = nullptr;
   constexpr int VEC = 16 / sizeof(T);
   constexpr int SEGS = kHeadThreads / LPR;
   constexpr int D = LPR * VEC;
@@ -549,10 +564,14 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
   const int ps = a.page_size;
   const int32_t* pi = a.page_indices + b * a.pisb + kvh * a.pish;
   if (tid < kWaves * kBins) (&sh.hist[0][0])[tid] = 0;  // read after the phase-1 barriers
-  // phase 1: scores, the page table staged in LDS chunk by chunk
+  // phase 1: scores (and each head's running max), the page table staged in
+  // LDS chunk by chunk
+  float rmax[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) rmax[g] = -1.0e6f;
   if (kTableInLds) {
     // the whole page table is already in sh.s_pages (written by this workgroup)
-    score_rows<T, LPR, G, kHeadThreads, U>(a, b, kvh, 0, n, sc, stride, sh.s_pages, 0);
+    score_rows<T, LPR, G, kHeadThreads, U>(a, b, kvh, 0, n, sc, stride, sh.s_pages, 0, rmax);
   } else if (!a.scores_ready) {
     for (int cb = 0; cb < n; cb += kTablePages * ps) {
       const int ce = min(n, cb + kTablePages * ps);
@@ -561,8 +580,16 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
         for (int i = tid; i < np; i += kHeadThreads) sh.s_pages[i] = pi[cb / ps + i];
       }
       __syncthreads();
-      score_rows<T, LPR, G, kHeadThreads, U>(a, b, kvh, cb, ce, sc, stride, sh.s_pages, cb);
+      score_rows<T, LPR, G, kHeadThreads, U>(a, b, kvh, cb, ce, sc, stride, sh.s_pages, cb,
+                                             rmax);
       __syncthreads();
+    }
+  }
+  if (sh.wmax) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float m = wave_max(rmax[g]);
+      if (lane == 0) sh.wmax[g * kWaves + wid] = m;
     }
   }
   __syncthreads();
@@ -692,7 +719,9 @@ __global__ __launch_bounds__(kHeadThreads) void decode_head_kernel(DecodeArgs a)
   __shared__ int flag_cnt[kWaves];
   __shared__ float red[kWaves * D];
   __shared__ int s_pages[kTablePages];
-  const HeadShared sh{hist, part, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
+  __shared__ float wmax[G * kWaves];
+  HeadShared sh{hist, part, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
+  sh.wmax = wmax;
 
   const int bkv = blockIdx.x;
   const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
@@ -736,7 +765,9 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
   __shared__ int flag_cnt[kWaves];
   __shared__ float red[kWaves * D];
   __shared__ int s_pages[kTablePages];
-  const HeadShared sh{hist, part, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
+  __shared__ float wmax[G * kWaves];
+  HeadShared sh{hist, part, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
+  sh.wmax = wmax;
 
   const int bkv = blockIdx.x;
   const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
@@ -799,8 +830,10 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
   __shared__ float s_th[G], s_sg[G], s_tin[G];
   __shared__ float scratch[kWaves];
   __shared__ float ups[G][kWaves];
+  __shared__ float wmax[G * kWaves];
   HeadShared sh{hist, part, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
   sh.tau_in_lds = s_tin;
+  sh.wmax = wmax;
 
   const int tid = threadIdx.x, wid = tid >> 6;
   const int bkv = blockIdx.x;
