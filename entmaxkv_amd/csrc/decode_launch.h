@@ -60,7 +60,10 @@ int Launch<T, G>::topk(DecodeArgs a, SelectArgs t, int B, int Hkv, int D, int to
   *handled = 0;
   return dispatch_lpr<T>(D, [&](auto lpr) {
     constexpr int LPR = decltype(lpr)::value;
-    constexpr int UC = G >= 8 ? 1 : (G == 1 ? 4 : 8 / G);
+    // pages per row segment in flight in the criticality scan: two measured
+    // faster than four for a lone group (more requests in flight per CU only
+    // queue up); the G query heads of a group share every page load
+    constexpr int UC = G >= 8 ? 1 : (G == 1 ? 2 : 8 / G);
     constexpr int UD = G >= 4 ? 2 : 8 / G;
     auto kern = topk_decode_kernel<T, LPR, G, UC, UD>;
     const int64_t avail = lds_left((const void*)kern, "topk_decode_kernel");

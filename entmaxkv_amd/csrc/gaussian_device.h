@@ -25,11 +25,18 @@
 namespace ekv {
 namespace gauss {
 
-// Workgroups per (b, kv head) of the moments launch: about 1024 workgroups in
-// all, at least 64 pages each, at most 64 per head.
-inline int moment_splits(int bkv, int pages) {
-  int s = (1024 + bkv - 1) / bkv;
-  const int by_pages = (pages + 63) / 64;
+// Threads per workgroup of the moments launch for GQA group G: 1024 (one
+// workgroup streaming a head's contiguous statistics measured faster than
+// four of 256 threads) unless the G query heads' registers need more than
+// 1024 threads leave (G >= 4: 256 threads).
+constexpr int moment_threads(int G) { return G <= 2 ? 1024 : 256; }
+
+// Workgroups per (b, kv head) of the moments launch: about 256K threads in
+// all, at least 256 pages each, at most 64 per head.
+inline int moment_splits(int bkv, int pages, int G) {
+  const int target = (256 * 1024) / moment_threads(G);
+  int s = (target + bkv - 1) / bkv;
+  const int by_pages = (pages + 255) / 256;
   if (s > by_pages) s = by_pages;
   if (s > 64) s = 64;
   return s < 1 ? 1 : s;
