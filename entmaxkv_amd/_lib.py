@@ -57,9 +57,14 @@ SIGNATURES = {
                                      P, P, P, I, I, P, F, F, P, P, P]),
     "ekv_tau_clamp": (I, [P, P, P, P, I64, I64, I, P, I64, I64, P, P, I, I, I, I, F, F, F, P]),
     "ekv_cache_seqlens_from_counts": (I, [P, P, I, I, I, P]),
+    "ekv_dense_decode_workspace_bytes": (I64, [I, I, I64]),
+    "ekv_dense_entmax_decode": (I, [P, I64, I64, P, P, I64, I64, I64, I64, P, P, I64, I64, P, P,
+                                    P, I, P, I64, I64, F, F, I, I, I, I, P, I64, I, P]),
+    "ekv_entmax_rows_forward": (I, [P, I64, P, I64, I64, I, F, P, I, P]),
+    "ekv_entmax_rows_backward": (I, [P, I64, P, I64, P, I64, I64, I, F, I, P]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib = None

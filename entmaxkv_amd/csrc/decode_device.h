@@ -71,6 +71,9 @@ struct DecodeArgs {
   int64_t csb, csh;
   const int32_t* q_seqlens;
   const float* slopes;
+  // ALiBi key positions [B, Hkv, rows] (null: a key's position is its cache row)
+  const int32_t* positions = nullptr;
+  int64_t posb = 0, posh = 0;
   float* tau;           // [B, H] output
   const float* tau_in;  // [B, H] starting tau (given-tau mode)
   int tau_mode;         // 0 exact (histogram + bracketed Halley), 1 given tau (unbounded Halley)
@@ -154,23 +157,31 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
     for (int g = 0; g < G; ++g) slope[g] = a.slopes[h0 + g] * (a.alpha - 1.0f);
   }
   const T* kh = (const T*)a.k + b * a.ksb + kvh * a.ksh;
+  const int32_t* kpos = a.slopes && a.positions ? a.positions + b * a.posb + kvh * a.posh : nullptr;
   const int ps = a.page_size;
+  constexpr int kNoRow = INT_MIN;
   // Rows of compacted tokens c0 + u * SEGS + seg and their K loads.  The loads
   // are unconditional (an invalid token re-reads row 0 and is masked), so
-  // all U of them are in flight together.
+  // all U of them are in flight together.  With explicit key positions the
+  // row is replaced by its position once the K load is issued.
   auto fetch = [&](int c0, int (&rows)[U], uint4 (&kv)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = c0 + u * SEGS + seg;
-      rows[u] = -1;
+      rows[u] = kNoRow;
       if (c < c_end) {
         const int page = pages[(c - c_base) / ps];
         const int64_t row = (int64_t)page * ps + (c % ps);
-        rows[u] = (page >= 0 && row < a.row_limit) ? (int)row : -1;
+        rows[u] = (page >= 0 && row < a.row_limit) ? (int)row : kNoRow;
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) kv[u] = ld16(kh + (int64_t)max(rows[u], 0) * a.ksr + col);
+    if (kpos) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (rows[u] != kNoRow) rows[u] = kpos[rows[u]];
+    }
   };
   auto consume = [&](int c0, const int (&rows)[U], const uint4 (&kv)[U]) {
 #pragma unroll
@@ -182,7 +193,7 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
         acc = seg_sum<LPR>(acc);
         if (c < c_end) {
           float s = acc;
-          if (rows[u] < 0) s = -INFINITY;
+          if (rows[u] == kNoRow) s = -INFINITY;
           else if (a.slopes) s += slope[g] * (float)(rows[u] - q_idx);
           if (sl == 0) sc[g * stride + c] = s;
           if (run_max) run_max[g] = fmaxf(run_max[g], s);

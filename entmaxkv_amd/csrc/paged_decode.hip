@@ -93,7 +93,8 @@ static int paged_decode(
     const int32_t* q_seqlens, const float* alibi_slopes, const float* tau_in, float* tau,
     int tau_mode, int iters, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha,
     float qscale, int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens,
-    void* workspace, int64_t workspace_bytes, int dtype, void* stream, bool force_split) {
+    void* workspace, int64_t workspace_bytes, int dtype, void* stream, bool force_split,
+    const int32_t* positions = nullptr, int64_t pos_stride_b = 0, int64_t pos_stride_h = 0) {
   EKV_REQUIRE(q && k && v && page_indices && cache_seqlens && tau && out && workspace,
               "ekv_paged_entmax_decode: null pointer");
   EKV_REQUIRE(B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0, "ekv_paged_entmax_decode: bad heads");
@@ -111,6 +112,9 @@ static int paged_decode(
                                   alibi_slopes, tau_in, tau, tau_mode, iters, out, out_stride_b,
                                   out_stride_h, alpha, qscale, page_size, H, Hkv, splits,
                                   max_tokens, workspace);
+  a.positions = positions;
+  a.posb = pos_stride_b;
+  a.posh = pos_stride_h;
   hipStream_t s = (hipStream_t)stream;
   const int G = H / Hkv;
   const bool head_path = one_workgroup_per_head(B * Hkv, force_split);
@@ -330,4 +334,68 @@ extern "C" int ekv_gaussian_paged_entmax_decode(
       return dec::Launch<T, decltype(gv)::value>::gaussian(a, f, B, Hkv, D, max_tokens, s);
     });
   });
+}
+
+// ---------------------------------------------------------------------------
+// dense (non-paged) decode: kernels/adadecode.py:754-1016
+// ---------------------------------------------------------------------------
+
+namespace {
+
+// The contiguous cache is read through the paged decode with an identity page
+// table; pages are grouped so that the table always fits the LDS staging
+// table (kTablePages entries).
+struct DenseGeom {
+  int page_size, n_slots, max_tokens;
+  int64_t score_bytes, total_bytes;
+};
+
+DenseGeom dense_geom(int B, int H, int64_t kv_rows) {
+  DenseGeom g;
+  g.page_size = 16;
+  while ((kv_rows + g.page_size - 1) / g.page_size > kTablePages) g.page_size *= 2;
+  g.n_slots = (int)((kv_rows + g.page_size - 1) / g.page_size);
+  g.max_tokens = g.n_slots * g.page_size;
+  g.score_bytes = ekv_decode_workspace_bytes(B, H, H, 0, 1, g.max_tokens);
+  g.total_bytes = g.score_bytes + ((int64_t)g.n_slots * 4 + 255) / 256 * 256;
+  return g;
+}
+
+__global__ void iota_kernel(int32_t* __restrict__ p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = i;
+}
+
+}  // namespace
+
+extern "C" int64_t ekv_dense_decode_workspace_bytes(int B, int H, int64_t kv_rows) {
+  if (B <= 0 || H <= 0 || kv_rows <= 0 || kv_rows > INT_MAX / 2) return -1;
+  return dense_geom(B, H, kv_rows).total_bytes;
+}
+
+extern "C" int ekv_dense_entmax_decode(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k, const void* v,
+    int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+    const int32_t* cache_seqlens, const int32_t* token_positions, int64_t pos_stride_b,
+    int64_t pos_stride_h, const int32_t* q_seqlens, const float* alibi_slopes, float* tau,
+    int iters, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale,
+    int B, int H, int Hkv, int D, void* workspace, int64_t workspace_bytes, int dtype,
+    void* stream) {
+  EKV_REQUIRE(q && k && v && cache_seqlens && tau && out && workspace,
+              "ekv_dense_entmax_decode: null pointer");
+  EKV_REQUIRE(B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0, "ekv_dense_entmax_decode: bad heads");
+  EKV_REQUIRE(kv_rows > 0 && kv_rows <= INT_MAX / 2, "ekv_dense_entmax_decode: bad kv_rows");
+  const DenseGeom g = dense_geom(B, H, kv_rows);
+  EKV_REQUIRE(workspace_bytes >= g.total_bytes, "ekv_dense_entmax_decode: workspace too small");
+  int32_t* table = (int32_t*)((char*)workspace + g.score_bytes);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(iota_kernel, dim3((g.n_slots + 255) / 256), dim3(256), 0, s, table,
+                     g.n_slots);
+  if (int rc = check_launch("iota_kernel")) return rc;
+  return paged_decode(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h, kv_stride_row,
+                      kv_rows, table, 0, 0, g.n_slots, cache_seqlens, 1, 0, q_seqlens,
+                      alibi_slopes, nullptr, tau, 0, iters, out, out_stride_b, out_stride_h,
+                      alpha, qscale, g.page_size, B, H, Hkv, D, splits_for(g.max_tokens),
+                      g.max_tokens, workspace, g.score_bytes, dtype, stream, false,
+                      alibi_slopes ? token_positions : nullptr, pos_stride_b, pos_stride_h);
 }

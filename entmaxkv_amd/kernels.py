@@ -142,7 +142,7 @@ def topk_pages(scores: torch.Tensor, k: int, num_kv_heads: int, last_page: int =
 # ---------------------------------------------------------------------------
 
 class DecodeWorkspace:
-    """Zero-initialised device workspace for one decode shape (counters return to 0)."""
+    """Device workspace for one decode shape (score spill rows; needs no initialisation)."""
 
     def __init__(self, batch, nheads, num_kv_heads, dim, splits, max_tokens, device):
         self.spec = (batch, nheads, num_kv_heads, dim, splits, max_tokens, torch.device(device))
@@ -331,6 +331,112 @@ def sparse_attention_decode_paged_gaussian_tau(q, k_cache, v_cache, out, cache_s
     assert tuple(tau.shape) == (batch, nheads), "tau must be [B, H]"
     paged_entmax_decode(q, k_cache, v_cache, out, cache_seqlens, page_indices, page_size, alpha,
                         1, tau_correction_iters, tau, alibi_slopes, q_seqlens, workspace)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# dense (non-paged) decode (kernels/adadecode.py:754-1016)
+# ---------------------------------------------------------------------------
+
+class DenseDecodeWorkspace:
+    """Device workspace of the dense decode for one (B, H, kv_rows) shape."""
+
+    def __init__(self, batch, nheads, kv_rows, device):
+        self.spec = (batch, nheads, kv_rows, torch.device(device))
+        nbytes = lib().ekv_dense_decode_workspace_bytes(batch, nheads, kv_rows)
+        if nbytes < 0:
+            raise ValueError(f"unsupported dense decode shape {self.spec[:3]}")
+        self.buf = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+
+
+def sparse_attention_decode_orchestrator(q, k_cache, v_cache, out, cache_seqlens,
+                                         token_positions, alibi_slopes=None,
+                                         is_causal: bool = True, alpha: float = 1.5,
+                                         niter: int = 10, max_splits: int = 32, bins: int = 16,
+                                         q_seqlens=None, profile: dict | None = None,
+                                         workspace: DenseDecodeWorkspace | None = None,
+                                         taus_out: torch.Tensor | None = None):
+    """Dense alpha-entmax decode over a contiguous cache (kernels/adadecode.py:754-1016).
+
+    q [B, H, 1, D]; k_cache, v_cache [B, Hkv, S, D] (the reference requires
+    Hkv == H; H a multiple of Hkv is accepted here); cache_seqlens [B]: head
+    (b, h) attends to keys [0, cache_seqlens[b]).  token_positions [B, Hkv, S]
+    (int) give the keys' positions for ALiBi, and the query sits at
+    q_seqlens[b] - 1 (q_seqlens defaults to cache_seqlens, :787-791).  tau is
+    the 16-bin histogram init plus ``niter`` bracketed Halley steps, as the
+    reference's stages 1-5; the output is the unnormalised weighted sum of
+    stages 6a/6b.  ``is_causal`` has no effect in the reference's kernels
+    (the causal masks are commented out, :530, :696-697) nor here;
+    ``max_splits`` is the reference's launch width and does not change
+    results here (the native launch sizes itself); only ``bins == 16`` is
+    supported.  ``profile`` (a dict) accumulates the step's device time in
+    ms under "total" and counts calls under "_count", as the reference's
+    per-stage dict does (:1008-1012); the step is one native launch sequence
+    so per-stage keys do not exist.
+    """
+    require_gpu(q, k_cache, v_cache, out, cache_seqlens)
+    batch, nheads, q_len, dim = q.shape
+    assert q_len == 1
+    num_kv_heads = k_cache.shape[1]
+    assert k_cache.shape[0] == batch, f"k_cache batch mismatch: {k_cache.shape[0]} != {batch}"
+    assert nheads % num_kv_heads == 0, "Query heads must be divisible by KV heads"
+    assert k_cache.shape[3] == dim, f"k_cache dim mismatch: {k_cache.shape[3]} != {dim}"
+    assert tuple(v_cache.shape) == tuple(k_cache.shape), "k_cache and v_cache shapes differ"
+    if bins != 16:
+        raise ValueError(f"bins={bins}: the native histogram init has 16 bins")
+    if niter < 0:
+        raise ValueError(f"niter must be >= 0 (got {niter})")
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+        raise TypeError("q, k_cache and v_cache must share a dtype")
+    kv_rows = k_cache.shape[2]
+    k = _row_major_d(k_cache, "k_cache")
+    v = _row_major_d(v_cache, "v_cache")
+    if k.stride() != v.stride():
+        v = v.contiguous()
+        k = k.contiguous()
+    q3 = _row_major_d(q[:, :, 0], "q")
+    o3 = out[:, :, 0]
+    direct = o3.stride(-1) == 1 and o3.data_ptr() % 16 == 0
+    o_target = o3 if direct else torch.empty(batch, nheads, dim, device=q.device, dtype=q.dtype)
+    csl = cache_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
+    assert tuple(csl.shape) == (batch,), "cache_seqlens must be [B]"
+    slopes = _alibi_f32(alibi_slopes, q.device)
+    pos = None
+    if slopes is not None and token_positions is not None:
+        pos = token_positions.to(device=q.device, dtype=torch.int32)
+        assert tuple(pos.shape) == (batch, num_kv_heads, kv_rows), \
+            "token_positions must be [B, H_kv, S]"
+        if pos.stride(-1) != 1:
+            pos = pos.contiguous()
+    qsl = None
+    if slopes is not None:
+        qsl = (q_seqlens if q_seqlens is not None else cache_seqlens)
+        qsl = qsl.to(device=q.device, dtype=torch.int32).contiguous()
+    if workspace is None or workspace.spec != (batch, nheads, kv_rows, q.device):
+        workspace = DenseDecodeWorkspace(batch, nheads, kv_rows, q.device)
+    taus = taus_out if taus_out is not None else torch.empty(batch, nheads, dtype=torch.float32,
+                                                             device=q.device)
+    assert tuple(taus.shape) == (batch, nheads) and taus.dtype == torch.float32 \
+        and taus.is_contiguous(), "taus_out must be a contiguous float32 [B, H] tensor"
+    events = None
+    if profile is not None:
+        events = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        events[0].record()
+    call("ekv_dense_entmax_decode",
+         q3.data_ptr(), q3.stride(0), q3.stride(1), k.data_ptr(), v.data_ptr(), k.stride(0),
+         k.stride(1), k.stride(2), kv_rows, csl.data_ptr(), ptr(pos),
+         0 if pos is None else pos.stride(0), 0 if pos is None else pos.stride(1), ptr(qsl),
+         ptr(slopes), taus.data_ptr(), int(niter), o_target.data_ptr(), o_target.stride(0),
+         o_target.stride(1), float(alpha), qscale_for(alpha, dim, q.dtype), batch, nheads,
+         num_kv_heads, dim, workspace.buf.data_ptr(), workspace.buf.numel(), dtype_code(q.dtype),
+         stream_ptr(q.device))
+    if not direct:
+        o3.copy_(o_target)
+    if events is not None:
+        events[1].record()
+        torch.cuda.synchronize(q.device)
+        profile["total"] = profile.get("total", 0.0) + events[0].elapsed_time(events[1])
+        profile["_count"] = profile.get("_count", 0) + 1
     return out
 
 

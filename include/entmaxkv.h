@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define EKV_ABI_VERSION 2
+#define EKV_ABI_VERSION 3
 
 const char* ekv_last_error(void);
 int ekv_abi_version(void);
@@ -224,6 +224,44 @@ int ekv_tau_clamp(const float* tau, const float* mu_p, const float* sigma_p,
 /* max(count - 1, 0) * page_size + last_page_size (kernels/selection_pack.py:7-20). */
 int ekv_cache_seqlens_from_counts(const int32_t* counts, int32_t* cache_seqlens, int n,
                                   int page_size, int last_page_size, void* stream);
+
+/* Dense (non-paged) decode: one query token per head over a contiguous cache
+ * k/v [B, Hkv, kv_rows, D] (row stride kv_stride_row, last dim contiguous),
+ * exact tau (histogram init + `iters` bracketed Halley steps, as tau_mode 0
+ * of ekv_paged_entmax_decode); head b, h attends to its first
+ * cache_seqlens[b] rows.  With alibi_slopes, key j of (b, kv head) sits at
+ * token_positions[b * pos_stride_b + kvh * pos_stride_h + j] (null: at j) and
+ * the query at q_seqlens[b] - 1 (null: cache_seqlens[b] - 1).  The final tau
+ * goes to tau [B, H].  Workspace: ekv_dense_decode_workspace_bytes bytes, no
+ * initialisation.  Replaces sparse_attention_decode_orchestrator
+ * (kernels/adadecode.py:754-1016). */
+int64_t ekv_dense_decode_workspace_bytes(int B, int H, int64_t kv_rows);
+int ekv_dense_entmax_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                            const void* k, const void* v, int64_t kv_stride_b,
+                            int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+                            const int32_t* cache_seqlens, const int32_t* token_positions,
+                            int64_t pos_stride_b, int64_t pos_stride_h,
+                            const int32_t* q_seqlens, const float* alibi_slopes, float* tau,
+                            int iters, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                            float alpha, float qscale, int B, int H, int Hkv, int D,
+                            void* workspace, int64_t workspace_bytes, int dtype, void* stream);
+
+/* Row-wise alpha-entmax over the last dimension: y[r] = entmax_alpha(x[r]) for
+ * `rows` rows of n elements (row strides in elements, elements contiguous),
+ * tau solved exactly (alpha 2 and 1.5: support refinement to the closed-form
+ * root; other alpha: bracketed Halley to fp32 resolution); tau_out [rows]
+ * (optional) receives the threshold on the (alpha - 1) x scale.  Replaces
+ * _fwd_entmax (kernels/triton_entmax.py:364-533). */
+int ekv_entmax_rows_forward(const void* x, int64_t x_row_stride, void* y, int64_t y_row_stride,
+                            int64_t rows, int n, float alpha, float* tau_out, int dtype,
+                            void* stream);
+
+/* Gradient of row-wise alpha-entmax: u = y^(2 - alpha) on the support,
+ * dx = u dy - (sum u dy / sum u) u.  Replaces _bwd_entmax
+ * (kernels/triton_entmax.py:536-612). */
+int ekv_entmax_rows_backward(const void* y, int64_t y_row_stride, const void* dy,
+                             int64_t dy_row_stride, void* dx, int64_t dx_row_stride,
+                             int64_t rows, int n, float alpha, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -500,6 +500,72 @@ def entmax_exact(s: np.ndarray, alpha: float) -> np.ndarray:
     return entmax_weights(np.asarray(s, np.float64), t, alpha)
 
 
+def entmax_rows(x: np.ndarray, alpha: float) -> np.ndarray:
+    """Row-wise alpha-entmax over the last axis of x (unscaled inputs).
+
+    kernels/triton_entmax.py:364-533 scales x by (alpha-1) (:401-409, :472)
+    and writes [z - tau]_+^(1/(alpha-1)) (:514-533) after ``n_iter`` hybrid
+    steps; this restatement uses the exact tau (entmax_exact), the limit the
+    reference's iterations approach.  Pinned by: entmax_tau_exact's checks.
+    """
+    x = np.asarray(x, np.float64)
+    flat = x.reshape(-1, x.shape[-1])
+    out = np.stack([entmax_exact((alpha - 1.0) * r, alpha) for r in flat])
+    return out.reshape(x.shape)
+
+
+def entmax_rows_backward(y: np.ndarray, dy: np.ndarray, alpha: float) -> np.ndarray:
+    """Vector-Jacobian product of row-wise entmax at output y.
+
+    kernels/triton_entmax.py:536-612: u = y^(2-alpha) on {y > 0},
+    dx = u * dy - (sum u dy / sum u) * u.  Pinned by: central finite
+    differences of entmax_rows (tests).
+    """
+    y = np.asarray(y, np.float64)
+    dy = np.asarray(dy, np.float64)
+    u = np.where(y > 0, np.abs(y) ** (2.0 - alpha), 0.0)
+    scalar = (u * dy).sum(-1, keepdims=True) / u.sum(-1, keepdims=True)
+    return u * dy - scalar * u
+
+
+def dense_entmax_decode(q, K, V, cache_seqlens, alpha, niter, dtype, alibi_slopes=None,
+                        token_positions=None, q_seqlens=None):
+    """Dense (non-paged) decode of kernels/adadecode.py:754-1016, float64.
+
+    Head (b, h) attends to rows [0, cache_seqlens[b]) of K[b, h // G]; scores
+    use the dtype-rounded scaled query (:161-163); ALiBi adds
+    (alpha-1) * slope_h * (token_positions[b, kvh, j] - q_idx) with
+    q_idx = q_seqlens[b] - 1, q_seqlens defaulting to cache_seqlens (:188-205,
+    :787-791); tau from the 16-bin histogram init and ``niter`` bracketed
+    Halley steps (:382-592); out = sum_j [s_j - tau]_+^(1/(alpha-1)) v_j.
+    q: [B, H, D]; K, V: [B, Hkv, S, D].  Returns (out [B, H, D], tau [B, H]).
+    Pinned by: paged_entmax_decode with an identity page table (same tokens,
+    same tau trajectory) and entmax_exact once converged (tests).
+    """
+    B, H, D = q.shape
+    Hkv = K.shape[1]
+    G = H // Hkv
+    qs = scaled_query(q, alpha, dtype)
+    out = np.zeros((B, H, D))
+    taus = np.zeros((B, H))
+    for b in range(B):
+        n = int(cache_seqlens[b])
+        q_idx = int(q_seqlens[b] if q_seqlens is not None else cache_seqlens[b]) - 1
+        for h in range(H):
+            kvh = h // G
+            rows = np.arange(n)
+            s = np.asarray(K[b, kvh], np.float64)[rows] @ np.asarray(qs[b, h], np.float64)
+            if alibi_slopes is not None:
+                slope = float(np.float32(np.float32(alibi_slopes[h]) * np.float32(alpha - 1.0)))
+                pos = rows if token_positions is None else np.asarray(token_positions[b, kvh])[rows]
+                s = s + slope * (pos.astype(np.float64) - q_idx)
+            t = solve_tau_exact_iterative(s, alpha, niter)
+            p = entmax_weights(s, t, alpha)
+            out[b, h] = p @ np.asarray(V[b, kvh], np.float64)[rows] if n else 0.0
+            taus[b, h] = t
+    return out, taus
+
+
 # ---------------------------------------------------------------------------
 # a7: Gaussian page statistics
 # ---------------------------------------------------------------------------

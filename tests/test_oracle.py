@@ -389,3 +389,86 @@ def test_config1_cpu_topk_step():
         dense = O.entmax_exact(K[0, h] @ qs[0, h], 1.5) @ V[0, h]
         rels.append(np.linalg.norm(out[0, h] - dense) / np.linalg.norm(dense))
     assert max(rels) < 2.0 * (1.0 - budget / (S - 1))
+
+
+# ---------------------------------------------------------------------------
+# dense utilities: row-wise entmax backward, dense decode
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("alpha", [1.5, 2.0, 1.25])
+def test_entmax_rows_backward_vs_finite_differences(alpha):
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((3, 40)) * 2.0
+    dy = rng.standard_normal((3, 40))
+    y = O.entmax_rows(x, alpha)
+    dx = O.entmax_rows_backward(y, dy, alpha)
+    eps = 1e-6
+    for r in range(3):
+        for j in range(40):
+            xp = x.copy()
+            xm = x.copy()
+            xp[r, j] += eps
+            xm[r, j] -= eps
+            fd = ((O.entmax_rows(xp[r], alpha) - O.entmax_rows(xm[r], alpha)) @ dy[r]) / (2 * eps)
+            assert abs(fd - dx[r, j]) < 1e-5, (r, j, fd, dx[r, j])
+    # gradients of a probability map sum to zero along the row
+    np.testing.assert_allclose(dx.sum(-1), 0.0, atol=1e-12)
+
+
+def test_entmax_rows_scaling():
+    # the (alpha - 1) input scale: sparsemax of x equals entmax_exact of x itself,
+    # 1.5-entmax of x equals entmax_exact of x / 2
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal(50)
+    np.testing.assert_allclose(O.entmax_rows(x, 2.0), O.entmax_exact(x, 2.0))
+    np.testing.assert_allclose(O.entmax_rows(x, 1.5), O.entmax_exact(x / 2, 1.5))
+    np.testing.assert_allclose(O.entmax_rows(x[None], 1.5).sum(), 1.0, atol=1e-12)
+
+
+def _dense_case(rng, B=2, Hkv=2, G=2, S=300, D=32, dtype="fp32"):
+    K = O.round_to(rng.standard_normal((B, Hkv, S, D)), dtype)
+    V = O.round_to(rng.standard_normal((B, Hkv, S, D)), dtype)
+    q = O.round_to(rng.standard_normal((B, Hkv * G, D)), dtype)
+    return K, V, q
+
+
+@pytest.mark.parametrize("alpha", [1.5, 2.0])
+@pytest.mark.parametrize("alibi", [False, True])
+def test_dense_decode_is_paged_decode_with_identity_table(alpha, alibi):
+    rng = np.random.default_rng(23)
+    K, V, q = _dense_case(rng)
+    B, Hkv, S, _ = K.shape
+    H = q.shape[1]
+    lens = np.array([300, 173])
+    slopes = rng.uniform(0.01, 0.2, H) if alibi else None
+    out, tau = O.dense_entmax_decode(q, K, V, lens, alpha, 2, "fp32", alibi_slopes=slopes)
+    ps = 16
+    P = (S + ps - 1) // ps
+    pidx = np.broadcast_to(np.arange(P), (B, Hkv, P))
+    seq2 = np.repeat(lens[:, None], Hkv, 1)
+    ref, ref_tau = O.paged_entmax_decode(q, K, V, pidx, seq2, ps, alpha, 2, "fp32",
+                                         alibi_slopes=slopes, q_seqlens=lens)
+    np.testing.assert_allclose(out, ref, atol=1e-12)
+    np.testing.assert_allclose(tau, ref_tau, atol=1e-12)
+
+
+def test_dense_decode_position_shift_invariance():
+    # shifting every key position by c shifts every ALiBi score by the same
+    # amount: the output is unchanged and tau moves by (alpha-1)*slope*c
+    rng = np.random.default_rng(24)
+    K, V, q = _dense_case(rng)
+    B, Hkv, S, _ = K.shape
+    H = q.shape[1]
+    lens = np.array([300, 250])
+    slopes = rng.uniform(0.01, 0.2, H)
+    pos = np.sort(rng.choice(4 * S, (B, Hkv, S)), axis=-1)
+    o1, t1 = O.dense_entmax_decode(q, K, V, lens, 1.5, 30, "fp32", slopes, pos, lens + 900)
+    o2, t2 = O.dense_entmax_decode(q, K, V, lens, 1.5, 30, "fp32", slopes, pos + 37, lens + 900)
+    np.testing.assert_allclose(o1, o2, atol=1e-9)
+    sl = np.float32(slopes.astype(np.float32) * np.float32(0.5)).astype(np.float64)
+    np.testing.assert_allclose(t2 - t1, np.broadcast_to(sl * 37, t1.shape), atol=1e-9)
+    # converged: exact entmax over the biased scores
+    qs = O.scaled_query(q, 1.5, "fp32")
+    b, h = 1, 3
+    s = K[b, h // 2][:250] @ qs[b, h] + sl[h] * (pos[b, h // 2][:250] - (250 + 900 - 1))
+    np.testing.assert_allclose(o1[b, h], O.entmax_exact(s, 1.5) @ V[b, h // 2][:250], atol=1e-9)
