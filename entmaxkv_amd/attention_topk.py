@@ -32,7 +32,8 @@ def sparse_attention_decode_paged(
     when a head does not fit one workgroup's LDS or the batch is small).  ``cache_seqlens`` is the compacted token count supplied by the
     caller, as in the reference (n_selected * page_size + last_page_size).
     ``splits`` and ``use_triton_criticality`` are accepted for compatibility.
-    Under GQA the page table is per kv head (group maximum of page scores).
+    Under GQA the page table is per kv head: the k pages of best rank over the
+    group's query heads (round robin over each head's own page order).
     Ragged cache (``kv_cache.seq_lens``): each sequence selects
     min(budget // ps, P_b - 1) pages of its own; ``cache_seqlens`` may then be
     None (derived per sequence, ``PagedKVCache.compacted_seqlens``) and

@@ -4,9 +4,9 @@
 //   (+ fp32 ALiBi bonus), fp32 accumulation, stored in the query dtype.
 //   Follows kernels/page_criticality.py:24-104,142-187 (scale 1.0).
 // top-k: per (b, kv head) the k pages with the largest score (under GQA the
-//   group maximum of the query heads' scores), packed in ascending page order,
-//   ties broken toward the lower page index, followed by the last-page
-//   sentinel.  Replaces torch.topk + the index buffer of attention_topk.py:52-71
+//   k pages of best rank over the query heads' own orders, ties to the lower
+//   page index), packed in ascending page order, ties broken toward the lower
+//   page index, followed by the last-page sentinel.  Replaces torch.topk + the index buffer of attention_topk.py:52-71
 //   and kv_cache.py:167-185.
 //
 // Ragged batches (seq_lens non-null): every (b, kv head) scores, selects and
@@ -42,7 +42,7 @@ using namespace ekv::topk;
 
 // One workgroup of kHeadThreads per (b, kv head): scores every page of the
 // head (16-byte loads, kHeadUnroll pages per row segment in flight), keeps
-// the group-max keys in LDS and, when k_sel >= 0, selects the top-k pages in
+// the page keys in LDS (G == 1) and, when k_sel >= 0, selects the top-k pages in
 // the same workgroup.  No cross-workgroup communication.
 constexpr int kHeadThreads = 512;
 constexpr int kHeadUnroll = 8;
@@ -59,7 +59,8 @@ __global__ __launch_bounds__(kHeadThreads) void criticality_head_kernel(
   const int bkv = blockIdx.x;
   const int b = bkv / Hkv, kvh = bkv % Hkv;
   const Ragged r = ragged_topk(seq_lens, b, page_size, stride, seq_len, q_pos, k_sel, last_page);
-  const bool keep_keys = r.k >= 0 && r.count <= lds_key_cap;
+  // G > 1 keeps its page ranks and candidate list in LDS instead of keys
+  const bool keep_keys = G == 1 && r.k >= 0 && r.count <= lds_key_cap;
   EKV_CSTAMP(0);
   T* sbase = criticality_scan_head<T, LPR, G, kHeadThreads, U>(
       q, qsb, qsh, kmin, kmax, ssb, ssh, ssp, slopes, scores, H, stride, r.count, page_size,
@@ -69,7 +70,8 @@ __global__ __launch_bounds__(kHeadThreads) void criticality_head_kernel(
   EKV_CSTAMP(1);
   topk_select_block<T, G, kHeadThreads>(sbase, stride, r.count, r.k, r.last_page,
                                         page_indices + b * pisb + kvh * pish, lds_keys,
-                                        keep_keys ? r.count : 0, keep_keys);
+                                        G > 1 ? lds_key_cap : (keep_keys ? r.count : 0),
+                                        keep_keys, nullptr, lds_keys + stride);
 }
 
 template <typename T, int LPR, int G>
@@ -139,7 +141,31 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const T* __restrict__ sc
   const T* s0 = scores + ((int64_t)b * H + kvh * G) * stride;
   extern __shared__ uint32_t lds_keys[];
   topk_select_block<T, G, kThreads>(s0, stride, r.count, r.k, r.last_page,
-                                    page_indices + b * pisb + kvh * pish, lds_keys, lds_key_cap);
+                                    page_indices + b * pisb + kvh * pish, lds_keys, lds_key_cap,
+                                    false, nullptr, lds_keys + stride);
+}
+
+// Dynamic LDS of the top-k select over `num_pages` pages: the staged keys
+// (G == 1, when they fit) or the page ranks plus one candidate list (G > 1,
+// required).  Returns the bytes (0: none) or -1 when a G > 1 select does not
+// fit; `cap` receives the key capacity.
+int64_t select_lds_bytes(int G, int num_pages, int k, int* cap) {
+  if (G == 1) {
+    *cap = num_pages <= kMaxStagedKeys ? num_pages : 0;
+    return (int64_t)*cap * 4;
+  }
+  *cap = num_pages;
+  const int64_t bytes = ((int64_t)num_pages + group_list_words(G, k)) * 4;
+  return (num_pages <= kMaxStagedKeys && bytes <= kLdsPerWorkgroup - 8192) ? bytes : -1;
+}
+
+int set_lds(const void* kern, int64_t bytes, const char* what) {
+  if (bytes <= 65536) return EKV_OK;
+  const hipError_t e =
+      hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e != hipSuccess)
+    return set_error(EKV_ERR_HIP, "%s LDS %lld: %s", what, (long long)bytes, hipGetErrorString(e));
+  return EKV_OK;
 }
 
 template <typename F>
@@ -176,12 +202,21 @@ extern "C" int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q
       constexpr int LPR = decltype(lpr)::value;
       return dispatch_group(H / Hkv, [&](auto gv) {
         constexpr int G = decltype(gv)::value;
+        int cap = 0;
+        int64_t sel_lds = 0;
+        if (k_select >= 0) {
+          sel_lds = select_lds_bytes(G, num_pages, k_select, &cap);
+          EKV_REQUIRE(sel_lds >= 0,
+                      "ekv_page_criticality: group top-k of %d of %d pages does not fit LDS",
+                      k_select, num_pages);
+        }
         if (one_workgroup_per_head(B * Hkv, seq_lens != nullptr)) {
           // one workgroup per (b, kv head), top-k in the same launch
-          const int cap = (k_select >= 0 && num_pages <= kMaxStagedKeys) ? num_pages : 0;
           constexpr int U = G >= 8 ? 2 : 16 / G;
-          hipLaunchKernelGGL((criticality_head_kernel<T, LPR, G, U>), dim3(B * Hkv),
-                             dim3(kHeadThreads), (size_t)cap * sizeof(uint32_t), s, (const T*)q,
+          auto kern = criticality_head_kernel<T, LPR, G, U>;
+          if (int rc = set_lds((const void*)kern, sel_lds, "criticality_head_kernel")) return rc;
+          hipLaunchKernelGGL(kern, dim3(B * Hkv), dim3(kHeadThreads), (size_t)sel_lds, s,
+                             (const T*)q,
                              q_stride_b, q_stride_h, (const T*)kmin, (const T*)kmax, s_stride_b,
                              s_stride_h, s_stride_page, alibi_slopes, (T*)scores, H, Hkv, num_pages,
                              page_size, seq_len, q_pos, k_select, last_page, seq_lens,
@@ -199,11 +234,11 @@ extern "C" int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q
         if (k_select >= 0) {
           int rc = check_launch("criticality_kernel");
           if (rc) return rc;
-          const int cap2 = num_pages <= kMaxStagedKeys ? num_pages : 0;
-          hipLaunchKernelGGL((topk_kernel<T, G>), dim3(B * Hkv), dim3(kThreads),
-                             (size_t)cap2 * sizeof(uint32_t), s, (const T*)scores, H, Hkv,
-                             num_pages, k_select, last_page, page_size, seq_lens, page_indices,
-                             pi_stride_b, pi_stride_h, cap2);
+          auto kern = topk_kernel<T, G>;
+          if ((rc = set_lds((const void*)kern, sel_lds, "topk_kernel"))) return rc;
+          hipLaunchKernelGGL(kern, dim3(B * Hkv), dim3(kThreads), (size_t)sel_lds, s,
+                             (const T*)scores, H, Hkv, num_pages, k_select, last_page, page_size,
+                             seq_lens, page_indices, pi_stride_b, pi_stride_h, cap);
           return check_launch("topk_kernel");
         }
         return check_launch("criticality_kernel");
@@ -224,10 +259,15 @@ extern "C" int ekv_topk_pages(const void* scores, int B, int H, int Hkv, int num
     using T = decltype(tv);
     return dispatch_group(H / Hkv, [&](auto gv) {
       constexpr int G = decltype(gv)::value;
-      const int cap = num_pages <= kMaxStagedKeys ? num_pages : 0;
-      hipLaunchKernelGGL((topk_kernel<T, G>), dim3(B * Hkv), dim3(kThreads),
-                         (size_t)cap * sizeof(uint32_t), s, (const T*)scores, H, Hkv, num_pages, k,
-                         last_page, 1, nullptr, page_indices, pi_stride_b, pi_stride_h, cap);
+      int cap = 0;
+      const int64_t sel_lds = select_lds_bytes(G, num_pages, k, &cap);
+      EKV_REQUIRE(sel_lds >= 0, "ekv_topk_pages: group top-k of %d of %d pages does not fit LDS",
+                  k, num_pages);
+      auto kern = topk_kernel<T, G>;
+      if (int rc = set_lds((const void*)kern, sel_lds, "topk_kernel")) return rc;
+      hipLaunchKernelGGL(kern, dim3(B * Hkv), dim3(kThreads), (size_t)sel_lds, s,
+                         (const T*)scores, H, Hkv, num_pages, k, last_page, 1, nullptr,
+                         page_indices, pi_stride_b, pi_stride_h, cap);
       return check_launch("topk_kernel");
     });
   });

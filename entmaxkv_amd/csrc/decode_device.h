@@ -757,6 +757,7 @@ struct SelectArgs {
   int k;              // pages selected per (b, kv head)
   int last_page;      // appended at slot k (the sentinel), or -1
   int key_cap;        // page keys that fit the dynamic LDS
+  int head_keys;      // G > 1: every query head's page keys kept in LDS too
   const int32_t* seq_lens;  // [B] per-sequence lengths (ragged batch) or null
 };
 
@@ -786,16 +787,20 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
   const topk::Ragged r = topk::ragged_topk(t.seq_lens, b, a.page_size, t.num_pages, t.seq_len,
                                            t.q_pos, t.k, t.last_page);
   const bool keep = r.count <= t.key_cap;
+  // G > 1: [page ranks: num_pages][candidate list: 2k][head keys: G * num_pages]
+  uint32_t* list = keys + t.num_pages;
+  uint32_t* head_keys = G > 1 && t.head_keys ? list + topk::group_list_words(G, t.k) : nullptr;
   EKV_STAMP(0);
   const T* sbase = topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC>(
       (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
       a.slopes, (T*)t.scores, a.H, t.num_pages, r.count, a.page_size, r.seq_len, r.q_pos, b, kvh,
-      keep ? keys : nullptr);
+      G == 1 ? (keep ? keys : nullptr) : head_keys);
   __syncthreads();
   EKV_STAMP(1);
   int32_t* pi = const_cast<int32_t*>(a.page_indices) + b * a.pisb + kvh * a.pish;
   topk::topk_select_block<T, G, kHeadThreads>(sbase, t.num_pages, r.count, r.k, r.last_page, pi,
-                                              keys, keep ? r.count : 0, keep, s_pages);
+                                              keys, keep ? r.count : 0, keep, s_pages, list,
+                                              head_keys, t.num_pages);
   __syncthreads();
   EKV_STAMP(2);
   const int n = token_count(a, b, kvh);
@@ -959,7 +964,6 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
   }
 }
 
-constexpr int kLdsPerWorkgroup = 160 * 1024;
 constexpr int kStageBytes = 96 * 1024;
 
 

@@ -68,9 +68,18 @@ int Launch<T, G>::topk(DecodeArgs a, SelectArgs t, int B, int Hkv, int D, int to
     auto kern = topk_decode_kernel<T, LPR, G, UC, UD>;
     const int64_t avail = lds_left((const void*)kern, "topk_decode_kernel");
     if (avail < 0) return EKV_ERR_HIP;
-    const int64_t keys = (int64_t)t.num_pages * 4;
+    // keys (G == 1), or page ranks + candidate list (+ every head's keys when
+    // they fit, else the selection re-reads the scores) for G > 1; the decode
+    // scores reuse the same LDS afterwards
     const int64_t stage = (int64_t)tokens * G * 4;
-    const int64_t lds = keys > stage ? keys : stage;
+    const int64_t sel = ((int64_t)t.num_pages + topk::group_list_words(G, t.k)) * 4;
+    const int64_t sel_keys = sel + (G > 1 ? (int64_t)G * t.num_pages * 4 : 0);
+    t.head_keys = 0;
+    int64_t lds = sel > stage ? sel : stage;
+    if (G > 1 && (sel_keys > stage ? sel_keys : stage) <= avail) {
+      t.head_keys = 1;
+      lds = sel_keys > stage ? sel_keys : stage;
+    }
     if (lds > avail) return EKV_OK;  // too big: the caller falls back
     const int rc = set_dynamic_lds((const void*)kern, (size_t)lds, "topk_decode_kernel");
     if (rc) return rc;

@@ -359,6 +359,9 @@ int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 // Compute units of the current device (queried once per device).
 int device_cus();
+
+// LDS one workgroup can allocate (gfx950).
+constexpr int kLdsPerWorkgroup = 160 * 1024;
 // The fused one-workgroup-per-(b, kv head) launches win when there are at
 // least half as many heads as compute units: below that, a head's scan spread
 // over many workgroups finishes sooner.  Measured at 128 heads on 256 CUs

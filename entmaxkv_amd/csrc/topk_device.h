@@ -94,174 +94,272 @@ __device__ __forceinline__ void wave_hist_add(unsigned* hist, uint32_t bin, bool
   }
 }
 
-// Block-wide top-k over `num_pages` group keys; writes ascending indices to
-// out[0..k) (and lds_out[0..k) when non-null) and `last_page` to out[k] when
-// last_page >= 0.  blockDim == NT.  The keys come from `lds_keys` when
+// Radix select over the keys key_of(p), p in [0, n), for 0 < k < n: `thr`
+// is the k-th largest key and `kk` how many keys equal to it are taken (the
+// first ones in page order).  8 bits per pass from the top, kBits / 8 passes:
+// one histogram per pass (LDS atomics), then every wave scans the 256 bins
+// itself (DPP prefix sum + ballot) to find the bin of the k-th largest key, so
+// a pass costs one barrier.  `hist` must be zero and visible to every thread
+// on entry.
+template <int NT, int kBits, typename KeyOf>
+__device__ __forceinline__ void radix_threshold(KeyOf key_of, int n, int k,
+                                                unsigned (*hist)[256], uint32_t& thr,
+                                                int& kk) {
+  constexpr int kPasses = kBits / 8;
+  constexpr int kBatch = 8;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  uint32_t prefix = 0, pmask = 0;
+  kk = k;
+#pragma unroll
+  for (int pass = 0; pass < kPasses; ++pass) {
+    const int shift = kBits - 8 * (pass + 1);
+    for (int p0 = 0; p0 < n; p0 += NT * kBatch) {
+      uint32_t kv[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int p = p0 + j * NT + tid;
+        kv[j] = p < n ? key_of(p) : 0u;
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int p = p0 + j * NT + tid;
+        const bool act = p < n && (kv[j] & pmask) == prefix;
+        const uint32_t bin = (kv[j] >> shift) & 255u;
+        if (pass == 0) {
+          // wave-uniform: every lane takes part in the ballots
+          if (p0 + j * NT < n) wave_hist_add(hist[0], bin, act);
+        } else if (act) {
+          atomicAdd(&hist[pass][bin], 1u);
+        }
+      }
+    }
+    __syncthreads();
+    // lane l holds bins 255-4l .. 252-4l; the bin where the count from the
+    // top reaches kk is found by every wave independently
+    const int top = 255 - 4 * lane;
+    const int c0 = (int)hist[pass][top], c1 = (int)hist[pass][top - 1];
+    const int c2 = (int)hist[pass][top - 2], c3 = (int)hist[pass][top - 3];
+    const int sum = c0 + c1 + c2 + c3;
+    const int incl = wave_incl_scan(sum);
+    const int excl = incl - sum;
+    const uint64_t hit = __ballot(excl < kk && incl >= kk);
+    const int src = (int)__builtin_ctzll(hit);  // at least kk keys share the prefix
+    int e = excl, bin, rem;
+    if (e + c0 >= kk) {
+      bin = top;
+      rem = kk - e;
+    } else if ((e += c0) + c1 >= kk) {
+      bin = top - 1;
+      rem = kk - e;
+    } else if ((e += c1) + c2 >= kk) {
+      bin = top - 2;
+      rem = kk - e;
+    } else {
+      e += c2;
+      bin = top - 3;
+      rem = kk - e;
+    }
+    bin = __builtin_amdgcn_readlane(bin, src);
+    rem = __builtin_amdgcn_readlane(rem, src);
+    prefix |= ((uint32_t)bin) << shift;
+    pmask |= 255u << shift;
+    kk = rem;
+  }
+  thr = prefix;
+}
+
+// Emits the selected pages in ascending page order, emit(slot, p, key): every
+// page when `take_all`, else the keys above `thr` and the first `kk` equal to
+// it.  Each wave owns a contiguous range of pages; slots come from ballots and
+// the per-wave counts (`wave_cnt`, 2 * NT / 64 ints; one barrier).
+template <int NT, typename KeyOf, typename Emit>
+__device__ __forceinline__ void pack_selected(KeyOf key_of, int n, bool take_all, uint32_t thr,
+                                              int kk, int* wave_cnt, Emit emit) {
+  constexpr int W = NT / 64;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int per = (n + W - 1) / W;
+  const int pw0 = min(n, wid * per), pw1 = min(n, pw0 + per);
+  auto flags = [&](int p, bool& gt, bool& eq, uint32_t& key) {
+    gt = eq = false;
+    key = 0;
+    if (p < pw1) {
+      key = key_of(p);
+      if (take_all) {
+        gt = true;
+      } else {
+        gt = key > thr;
+        eq = key == thr;
+      }
+    }
+  };
+  int gt_n = 0, eq_n = 0;
+  for (int r0 = pw0; r0 < pw1; r0 += 64) {
+    bool gt, eq;
+    uint32_t key;
+    flags(r0 + lane, gt, eq, key);
+    gt_n += __popcll(__ballot(gt));
+    eq_n += __popcll(__ballot(eq));
+  }
+  if (lane == 0) {
+    wave_cnt[2 * wid] = gt_n;
+    wave_cnt[2 * wid + 1] = eq_n;
+  }
+  __syncthreads();
+  int gt_base = 0, eq_base = 0;
+  for (int w = 0; w < wid; ++w) {
+    gt_base += wave_cnt[2 * w];
+    eq_base += wave_cnt[2 * w + 1];
+  }
+  for (int r0 = pw0; r0 < pw1; r0 += 64) {
+    const int p = r0 + lane;
+    bool gt, eq;
+    uint32_t key;
+    flags(p, gt, eq, key);
+    const uint64_t mg = __ballot(gt), me = __ballot(eq);
+    const int gt_rank = gt_base + __popcll(mg & below);
+    const int eq_rank = eq_base + __popcll(me & below);
+    if (gt || (eq && eq_rank < kk)) emit(gt_rank + min(eq_rank, kk), p, key);
+    gt_base += __popcll(mg);
+    eq_base += __popcll(me);
+  }
+}
+
+// LDS words the select of a group of G query heads needs beyond the staged
+// keys: the candidate list of one head (page, key, rank) for G > 1.
+__host__ __device__ constexpr int group_list_words(int G, int k) { return G > 1 ? 3 * k : 0; }
+
+// Block-wide top-k of one (b, kv head) over `num_pages` pages; writes
+// ascending page ids to out[0..k) (and lds_out[0..k) when non-null) and
+// `last_page` to out[k] when last_page >= 0.  blockDim == NT.
+//
+// G == 1: the head's own order keys.  They come from `lds_keys` when
 // `prestaged`, are staged there first when they fit (`lds_cap` keys), and are
 // otherwise recomputed from the scores on every pass (the scores must be
 // visible to this workgroup: written by a previous launch or by this
 // workgroup).
 //
-// Radix select, 8 bits per pass from the top: one histogram per pass (LDS
-// atomics), then every wave scans the 256 bins itself (DPP prefix sum +
-// ballot) to find the bin of the k-th largest key, so a pass costs one
-// barrier.  The pack gives each wave a contiguous range of pages; ranks come
-// from ballots and the per-wave counts (one barrier).  Keys above the
-// threshold are all taken; of the keys equal to it, the first kk in page
-// order.
+// G > 1 (the group shares one page table; no reference counterpart): pages
+// are taken by their best rank over the group's query heads, ties to the lower
+// page index -- round robin over the heads' own top-k lists.  Per head: a
+// radix select gives its top-k list (page, key) in `lds_list`, each entry's
+// rank within the list is counted (the list is ascending in page order, so
+// equal keys rank by page; every thread counts a slice of the list for one
+// entry), and `lds_keys` (num_pages words, required:
+// lds_cap >= num_pages) keeps each page's minimum rank.  Ranks become keys
+// k - rank and one more select takes the k best.  A head's keys come from
+// `head_keys[g * hk_stride + p]` when non-null, else from the scores.
 template <typename T, int G, int NT = kThreads>
 __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int64_t head_stride,
                                                   int num_pages, int k, int last_page,
                                                   int32_t* __restrict__ out, uint32_t* lds_keys,
                                                   int lds_cap, bool prestaged = false,
-                                                  int* lds_out = nullptr) {
+                                                  int* lds_out = nullptr,
+                                                  uint32_t* lds_list = nullptr,
+                                                  const uint32_t* head_keys = nullptr,
+                                                  int hk_stride = 0) {
   constexpr int W = NT / 64;
-  constexpr int kPasses = ScoreKey<T>::kBits / 8;
+  constexpr int kBits = ScoreKey<T>::kBits;
+  constexpr int kPasses = kBits / 8;
   constexpr int kBatch = 8;
   __shared__ unsigned hist[kPasses][256];
   __shared__ int wave_cnt[2 * W];
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wid = tid >> 6;
   k = min(k, num_pages);
-  const bool staged = prestaged || num_pages <= lds_cap;
-  // group key of page p: the maximum over the group's query heads
-  auto gkey = [&](int p) -> uint32_t {
-    uint32_t kk = ScoreKey<T>::key(s0[p]);
-#pragma unroll
-    for (int g = 1; g < G; ++g) kk = max(kk, ScoreKey<T>::key(s0[g * head_stride + p]));
-    return kk;
-  };
-  auto key_of = [&](int p) -> uint32_t { return staged ? lds_keys[p] : gkey(p); };
-  for (int i = tid; i < kPasses * 256; i += NT) (&hist[0][0])[i] = 0u;
-  if (staged && !prestaged) {
-    for (int p0 = 0; p0 < num_pages; p0 += NT * kBatch) {
-      uint32_t kv[kBatch];
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int p = p0 + j * NT + tid;
-        kv[j] = p < num_pages ? gkey(p) : 0u;
-      }
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int p = p0 + j * NT + tid;
-        if (p < num_pages) lds_keys[p] = kv[j];
-      }
-    }
-  }
-  __syncthreads();
-
-  EKV_CSTAMP(2);
-  uint32_t thr = 0;
-  int kk = 0;  // how many pages with key == thr to take
   const bool take_all = (k == num_pages);
-  if (k > 0 && !take_all) {
-    uint32_t prefix = 0, pmask = 0;
-    kk = k;
-#pragma unroll
-    for (int pass = 0; pass < kPasses; ++pass) {
-      const int shift = ScoreKey<T>::kBits - 8 * (pass + 1);
+  auto emit_out = [&](int slot, int p, uint32_t) {
+    out[slot] = p;
+    if (lds_out) lds_out[slot] = p;
+  };
+  auto zero_hist = [&]() {
+    for (int i = tid; i < kPasses * 256; i += NT) (&hist[0][0])[i] = 0u;
+  };
+  if constexpr (G == 1) {
+    const bool staged = prestaged || num_pages <= lds_cap;
+    auto own = [&](int p) -> uint32_t { return ScoreKey<T>::key(s0[p]); };
+    auto key_of = [&](int p) -> uint32_t { return staged ? lds_keys[p] : own(p); };
+    zero_hist();
+    if (staged && !prestaged) {
       for (int p0 = 0; p0 < num_pages; p0 += NT * kBatch) {
         uint32_t kv[kBatch];
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
           const int p = p0 + j * NT + tid;
-          kv[j] = p < num_pages ? key_of(p) : 0u;
+          kv[j] = p < num_pages ? own(p) : 0u;
         }
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
           const int p = p0 + j * NT + tid;
-          const bool act = p < num_pages && (kv[j] & pmask) == prefix;
-          const uint32_t bin = (kv[j] >> shift) & 255u;
-          if (pass == 0) {
-            // wave-uniform: every lane takes part in the ballots
-            if (p0 + j * NT < num_pages) wave_hist_add(hist[0], bin, act);
-          } else if (act) {
-            atomicAdd(&hist[pass][bin], 1u);
-          }
+          if (p < num_pages) lds_keys[p] = kv[j];
         }
       }
-      __syncthreads();
-      // lane l holds bins 255-4l .. 252-4l; the bin where the count from the
-      // top reaches kk is found by every wave independently
-      const int top = 255 - 4 * lane;
-      const int c0 = (int)hist[pass][top], c1 = (int)hist[pass][top - 1];
-      const int c2 = (int)hist[pass][top - 2], c3 = (int)hist[pass][top - 3];
-      const int sum = c0 + c1 + c2 + c3;
-      const int incl = wave_incl_scan(sum);
-      const int excl = incl - sum;
-      const uint64_t hit = __ballot(excl < kk && incl >= kk);
-      const int src = (int)__builtin_ctzll(hit);  // at least kk keys share the prefix
-      int e = excl, bin, rem;
-      if (e + c0 >= kk) {
-        bin = top;
-        rem = kk - e;
-      } else if ((e += c0) + c1 >= kk) {
-        bin = top - 1;
-        rem = kk - e;
-      } else if ((e += c1) + c2 >= kk) {
-        bin = top - 2;
-        rem = kk - e;
-      } else {
-        e += c2;
-        bin = top - 3;
-        rem = kk - e;
-      }
-      bin = __builtin_amdgcn_readlane(bin, src);
-      rem = __builtin_amdgcn_readlane(rem, src);
-      prefix |= ((uint32_t)bin) << shift;
-      pmask |= 255u << shift;
-      kk = rem;
-    }
-    thr = prefix;
-  }
-  EKV_CSTAMP(3);
-  if (k > 0) {
-    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    const int per = (num_pages + W - 1) / W;
-    const int pw0 = min(num_pages, wid * per), pw1 = min(num_pages, pw0 + per);
-    auto flags = [&](int p, bool& gt, bool& eq) {
-      gt = eq = false;
-      if (p < pw1) {
-        if (take_all) {
-          gt = true;
-        } else {
-          const uint32_t key = key_of(p);
-          gt = key > thr;
-          eq = key == thr;
-        }
-      }
-    };
-    int gt_n = 0, eq_n = 0;
-    for (int r0 = pw0; r0 < pw1; r0 += 64) {
-      bool gt, eq;
-      flags(r0 + lane, gt, eq);
-      gt_n += __popcll(__ballot(gt));
-      eq_n += __popcll(__ballot(eq));
-    }
-    if (lane == 0) {
-      wave_cnt[2 * wid] = gt_n;
-      wave_cnt[2 * wid + 1] = eq_n;
     }
     __syncthreads();
-    int gt_base = 0, eq_base = 0;
-    for (int w = 0; w < wid; ++w) {
-      gt_base += wave_cnt[2 * w];
-      eq_base += wave_cnt[2 * w + 1];
-    }
-    for (int r0 = pw0; r0 < pw1; r0 += 64) {
-      const int p = r0 + lane;
-      bool gt, eq;
-      flags(p, gt, eq);
-      const uint64_t mg = __ballot(gt), me = __ballot(eq);
-      const int gt_rank = gt_base + __popcll(mg & below);
-      const int eq_rank = eq_base + __popcll(me & below);
-      if (gt || (eq && eq_rank < kk)) {
-        const int slot = gt_rank + min(eq_rank, kk);
-        out[slot] = p;
-        if (lds_out) lds_out[slot] = p;
+    EKV_CSTAMP(2);
+    uint32_t thr = 0;
+    int kk = 0;
+    if (k > 0 && !take_all) radix_threshold<NT, kBits>(key_of, num_pages, k, hist, thr, kk);
+    EKV_CSTAMP(3);
+    if (k > 0) pack_selected<NT>(key_of, num_pages, take_all, thr, kk, wave_cnt, emit_out);
+  } else {
+    uint32_t* level = lds_keys;
+    if (k > 0 && !take_all) {
+      for (int p = tid; p < num_pages; p += NT) level[p] = (uint32_t)k;
+      uint32_t* list_page = lds_list;
+      uint32_t* list_key = lds_list + k;
+      uint32_t* list_rank = lds_list + 2 * k;
+      const int slices = k < NT ? NT / k : 1;
+      const int per = (k + slices - 1) / slices;
+#pragma unroll 1
+      for (int g = 0; g < G; ++g) {
+        auto key_g = [&](int p) -> uint32_t {
+          return head_keys ? head_keys[g * hk_stride + p]
+                           : ScoreKey<T>::key(s0[g * head_stride + p]);
+        };
+        // the barrier also ends the previous head's use of the list
+        zero_hist();
+        for (int i = tid; i < k; i += NT) list_rank[i] = 0u;
+        __syncthreads();
+        uint32_t thr;
+        int kk;
+        radix_threshold<NT, kBits>(key_g, num_pages, k, hist, thr, kk);
+        pack_selected<NT>(key_g, num_pages, false, thr, kk, wave_cnt,
+                          [&](int slot, int p, uint32_t key) {
+                            list_page[slot] = (uint32_t)p;
+                            list_key[slot] = key;
+                          });
+        __syncthreads();
+        // thread t counts list entries [s * per, s * per + per) against
+        // entry t % k (slice s = t / k); the lanes of a wave read the same
+        // key at a time (LDS broadcast)
+        for (int w = tid; w < k * slices; w += NT) {
+          const int i = w % k, j0 = (w / k) * per, j1 = min(k, j0 + per);
+          const uint32_t ki = list_key[i];
+          uint32_t cnt = 0;
+          for (int j = j0; j < j1; ++j) {
+            const uint32_t kj = list_key[j];
+            cnt += (kj > ki) | ((kj == ki) & (j < i));
+          }
+          if (cnt) atomicAdd(&list_rank[i], cnt);
+        }
+        __syncthreads();
+        for (int i = tid; i < k; i += NT) atomicMin(&level[list_page[i]], list_rank[i]);
       }
-      gt_base += __popcll(mg);
-      eq_base += __popcll(me);
+      __syncthreads();
+      for (int p = tid; p < num_pages; p += NT) level[p] = (uint32_t)k - level[p];
+      zero_hist();
+      __syncthreads();
+      // keys k - rank <= k <= 16384 fit 16 bits
+      auto key_l = [&](int p) -> uint32_t { return level[p]; };
+      uint32_t thr;
+      int kk;
+      radix_threshold<NT, 16>(key_l, num_pages, k, hist, thr, kk);
+      pack_selected<NT>(key_l, num_pages, false, thr, kk, wave_cnt, emit_out);
+    } else if (k > 0) {
+      pack_selected<NT>([](int) -> uint32_t { return 0u; }, num_pages, true, 0u, 0, wave_cnt,
+                        emit_out);
     }
   }
   if (tid == 0 && last_page >= 0) {
@@ -273,8 +371,9 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
 
 // Criticality scan of one (b, kv head) by a workgroup of NT threads: scores
 // of the G query heads for pages [0, count) written to `scores`
-// ([B, H, stride], query dtype; count <= stride) and, when `lds_keys` is non-null, the
-// group-max order key of every page kept there.  A row segment of LPR lanes
+// ([B, H, stride], query dtype; count <= stride) and, when `lds_keys` is
+// non-null, the order keys kept there: lds_keys[p] for G == 1, lds_keys[g *
+// stride + p] per query head for G > 1.  A row segment of LPR lanes
 // owns one page and loads its min and max rows with 16-byte loads, U pages
 // per segment in flight.  Returns the head's score base pointer.
 template <typename T, int LPR, int G, int NT, int U>
@@ -329,10 +428,13 @@ __device__ __forceinline__ T* criticality_scan_head(
           acc = add_rn(acc, mul_rn(slope[g], (float)(last_pos - q_pos)));
         }
         const T sv = from_f<T>(acc);
-        key = max(key, ScoreKey<T>::key(sv));
-        if (p < num_pages && sl == 0) sbase[(int64_t)g * stride + p] = sv;
+        key = ScoreKey<T>::key(sv);
+        if (p < num_pages && sl == 0) {
+          sbase[(int64_t)g * stride + p] = sv;
+          if (G > 1 && keep_keys) lds_keys[g * stride + p] = key;
+        }
       }
-      if (keep_keys && p < num_pages && sl == 0) lds_keys[p] = key;
+      if (G == 1 && keep_keys && p < num_pages && sl == 0) lds_keys[p] = key;
     }
   }
   return sbase;

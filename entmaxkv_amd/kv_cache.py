@@ -210,8 +210,9 @@ class PagedKVCache:
     def select_topk(self, q: torch.Tensor, k: int, alibi_slopes=None) -> torch.Tensor:
         """Fused criticality + top-k page table [B, Hkv, k + 1] (last page at slot k).
 
-        Replaces attention_topk.py:45-71.  Under GQA a kv head's page score is
-        the maximum of its query heads' scores.  In a ragged batch sequence b
+        Replaces attention_topk.py:45-71.  Under GQA a kv head takes the k
+        pages of best rank over its query heads' own page orders (ties to the
+        lower page index).  In a ragged batch sequence b
         selects k_b = min(k, P_b - 1) pages, its last page at slot k_b.
         """
         B, H = q.shape[:2]

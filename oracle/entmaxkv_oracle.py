@@ -184,17 +184,44 @@ def topk_pages(scores: np.ndarray, k: int) -> np.ndarray:
     return out.reshape(*lead, k)
 
 
-def topk_gqa_group_scores(scores: np.ndarray, num_kv_heads: int) -> np.ndarray:
-    """Per-KV-head selection score under GQA: max over the group's query heads.
+def _page_order(row: np.ndarray) -> np.ndarray:
+    """Pages of one score row from best to worst in topk_pages' order (NaN
+    first, value descending, +0.0 before -0.0, lower index first)."""
+    idx = np.arange(row.size)
+    key = np.where(np.isnan(row), np.inf, row)
+    nanflag = np.isnan(row).astype(np.int64)
+    negzero = ((row == 0) & np.signbit(row)).astype(np.int64)
+    return np.lexsort((idx, negzero, -key, -nanflag))
+
+
+def topk_gqa_pages(scores: np.ndarray, num_kv_heads: int, k: int) -> np.ndarray:
+    """Top-k pages of each KV head under GQA, ascending: [B, Hkv, k].
 
     The reference cannot run GQA top-k (attention_topk.py:52-71 packs per
     query head while kernels/adadecode_paged.py:600 requires kv-head keyed
-    page tables).  This build's documented policy: a KV head's page score is
-    the maximum of its query heads' scores.  Reduces to the identity for MHA.
+    page tables).  This build's documented policy: a page's level is its best
+    rank over the group's query heads (rank r = the r-th page of that head's
+    topk_pages order), and the k pages of lowest level are taken, ties to the
+    lower page index -- a round robin over the heads' own rankings.  It
+    depends on each head's order only, so heads whose scores differ in scale
+    or offset share the table fairly.  Reduces to topk_pages for MHA.
+    Pinned by: topk_pages for G = 1, invariance to per-head positive affine
+    maps, each head's top floor(k/G) kept, and a literal round-robin
+    restatement on small inputs (tests).
     """
-    B, H, P = scores.shape
+    s = np.asarray(scores, np.float64)
+    B, H, P = s.shape
     G = H // num_kv_heads
-    return np.max(np.asarray(scores, np.float64).reshape(B, num_kv_heads, G, P), axis=2)
+    out = np.empty((B, num_kv_heads, k), dtype=np.int64)
+    for b in range(B):
+        for kvh in range(num_kv_heads):
+            level = np.full(P, P, dtype=np.int64)
+            for g in range(G):
+                rank = np.empty(P, dtype=np.int64)
+                rank[_page_order(s[b, kvh * G + g])] = np.arange(P)
+                level = np.minimum(level, rank)
+            out[b, kvh] = np.sort(np.lexsort((np.arange(P), level))[:k])
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -913,8 +940,7 @@ def topk_decode_step(q, K, V, stats, token_budget, page_size, alpha, niter,
     scores = page_criticality(q, kmin, kmax, dtype, num_pages=P - 1,
                               alibi_slopes=alibi_slopes, page_size=page_size,
                               seq_len=S, q_pos=S - 1)
-    group = topk_gqa_group_scores(scores, Hkv)
-    sel = topk_pages(group, k)
+    sel = topk_gqa_pages(scores, Hkv, k)
     pidx = np.concatenate([sel, np.full((B, Hkv, 1), P - 1)], axis=2)
     lps = S - (P - 1) * page_size
     seqlens = np.full((B, Hkv), k * page_size + lps)

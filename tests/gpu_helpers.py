@@ -47,3 +47,44 @@ def ulp_diff_16(a, b, dtype):
     mant = {"fp16": 10, "bf16": 7, "fp32": 23}[dtype]
     e = np.floor(np.log2(np.maximum(np.abs(b), 2.0 ** -14)))
     return np.abs(a - b) / 2.0 ** (e - mant)
+
+
+def gqa_structured_case(rng, B, Hkv, G, S, D, ps, dtype, n_own, n_shared, beta):
+    """GQA inputs where the group's query heads want different pages: per kv
+    head, n_shared pages pulled toward the group's mean query direction and
+    n_own pages per query head pulled toward that head's direction (keys +=
+    beta * direction); query norms differ per head (x0.5..2).  Returns float64
+    arrays q [B, H, D], k, v [B, Hkv, S, D] already rounded to ``dtype``."""
+    H = Hkv * G
+    P = S // ps
+    q = rng.standard_normal((B, H, D)) * rng.uniform(0.5, 2.0, (1, H, 1))
+    k = rng.standard_normal((B, Hkv, S, D))
+    v = rng.standard_normal((B, Hkv, S, D))
+    for b in range(B):
+        for kvh in range(Hkv):
+            pages = rng.choice(P - 1, n_shared + G * n_own, replace=False)
+            qh = [q[b, kvh * G + g] / np.linalg.norm(q[b, kvh * G + g]) for g in range(G)]
+            mean = sum(qh) / np.linalg.norm(sum(qh))
+            for i, p in enumerate(pages):
+                d = mean if i < n_shared else qh[(i - n_shared) // n_own]
+                k[b, kvh, p * ps:(p + 1) * ps] += beta * d
+    return O.round_to(q, dtype), O.round_to(k, dtype), O.round_to(v, dtype)
+
+
+def dense_entmax_attention(q, K, V, alpha, dtype):
+    """Exact entmax attention of every query head over all of its kv head's
+    keys (float64): the accuracy reference of the sparse decode steps."""
+    B, H, D = q.shape
+    G = H // K.shape[1]
+    qs = O.scaled_query(q, alpha, dtype)
+    out = np.zeros((B, H, D))
+    for b in range(B):
+        for h in range(H):
+            s = np.asarray(K[b, h // G], np.float64) @ qs[b, h]
+            out[b, h] = O.entmax_exact(s, alpha) @ np.asarray(V[b, h // G], np.float64)
+    return out
+
+
+def rel_error(out, ref):
+    """||out - ref|| / ||ref|| over the whole tensor (tests/benchmark_utils.py:38-49)."""
+    return float(np.linalg.norm(np.asarray(out) - ref) / np.linalg.norm(ref))

@@ -132,8 +132,7 @@ def test_criticality_and_topk(dtype, G, alibi, path):
     tol = 2.0 ** -20 * terms + ulp * np.abs(ref_scores)
     assert (np.abs(got_scores - ref_scores) <= tol).all()
     # the page table is bit-exact given the scores the kernel produced
-    group = O.topk_gqa_group_scores(got_scores, Hkv)
-    ref_sel = O.topk_pages(group, kk)
+    ref_sel = O.topk_gqa_pages(got_scores, Hkv, kk)
     got = to_np(pidx).astype(np.int64)
     np.testing.assert_array_equal(got[:, :, :kk], ref_sel)
     assert (got[:, :, kk] == P - 1).all()
@@ -349,7 +348,7 @@ def test_topk_api_end_to_end(dtype, G, path, alibi):
     ulp = {"fp16": 2.0 ** -10, "bf16": 2.0 ** -7, "fp32": 2.0 ** -23}[dtype]
     assert (np.abs(scores - ref_scores) <= 2.0 ** -20 * terms + ulp * np.abs(ref_scores)).all()
     # page table bit-exact given the kernel's scores
-    sel = O.topk_pages(O.topk_gqa_group_scores(scores, Hkv), n_sel)
+    sel = O.topk_gqa_pages(scores, Hkv, n_sel)
     pidx = np.concatenate([sel, np.full((B, Hkv, 1), P - 1)], axis=2)
     np.testing.assert_array_equal(to_np(cache._page_indices_buf).astype(np.int64), pidx)
     ref, _ = O.paged_entmax_decode(q[:, :, 0], Kf, Vf, pidx, np.full((B, Hkv), n_sel * ps + lps),

@@ -111,7 +111,7 @@ def test_ragged_topk_step(path, G, dtype):
         terms = np.abs(O.page_criticality(q[b:b + 1, :, 0], st[0], st[1], "fp32", num_pages=P - 1))
         ulp = {"fp16": 2.0 ** -10, "bf16": 2.0 ** -7, "fp32": 2.0 ** -23}[dtype]
         assert (np.abs(scores - ref_scores) <= 2.0 ** -20 * terms + ulp * np.abs(ref_scores)).all()
-        sel = O.topk_pages(O.topk_gqa_group_scores(scores, Hkv), n_sel)
+        sel = O.topk_gqa_pages(scores, Hkv, n_sel)
         pidx = np.concatenate([sel, np.full((1, Hkv, 1), P - 1)], axis=2)
         np.testing.assert_array_equal(table[b:b + 1, :, :n_sel + 1], pidx)
         lps = S_b - (P - 1) * ps
