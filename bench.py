@@ -53,10 +53,12 @@ def _args():
                         "outlier pages scaled x3 toward q (BASELINE config 3), iid = N(0, 1)")
     p.add_argument("--only", choices=["topk", "gaussian", "criticality"], default=None,
                    help="run one step kind in a loop (for profilers)")
-    p.add_argument("--config", choices=["headline", "c5"], default="headline",
+    p.add_argument("--config", choices=["headline", "c5", "dense", "rows"], default="headline",
                    help="c5: BASELINE config 5 instead of the headline line (ragged batch, "
                         "B=32, 32 q / 8 kv heads, bf16, lengths ~ U[4096, 131072], 1%% outlier "
-                        "pages x4, Gaussian alpha 1.5 with append over 16 consecutive steps)")
+                        "pages x4, Gaussian alpha 1.5 with append over 16 consecutive steps); "
+                        "dense: the dense (non-paged) decode over every token of the headline "
+                        "shape; rows: row-wise entmax forward + backward")
     p.add_argument("--copy-calib-mib", type=int, default=0,
                    help="with --only: first copy a buffer of this many MiB (a copy kernel of "
                         "known traffic that scales rocprofv3's FETCH_SIZE / WRITE_SIZE)")
@@ -210,6 +212,88 @@ def _config5(a):
     return 0
 
 
+def _config_dense(a):
+    """Dense (non-paged) decode at the headline shape: B=8, H=32, D=128, L=32768,
+    fp16, alpha 1.5, niter 2, every token attended.  Algorithmic bytes per
+    step: all K rows, the V rows of supported tokens (counted on the output's
+    tau), q and out."""
+    import torch
+
+    from entmaxkv_amd.kernels import DenseDecodeWorkspace, sparse_attention_decode_orchestrator
+
+    B, H, D, L, esz = a.batch, a.heads, a.head_dim, a.kv_len, 2
+    dt, dev = torch.float16, torch.device("cuda:0")
+    gd = torch.Generator(device=dev)
+    gd.manual_seed(1)
+    k = torch.randn(B, H, L, D, device=dev, dtype=dt, generator=gd)
+    v = torch.randn(B, H, L, D, device=dev, dtype=dt, generator=gd)
+    q = torch.randn(B, H, 1, D, device=dev, dtype=dt, generator=gd)
+    out = torch.zeros_like(q)
+    lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+    taus = torch.empty(B, H, dtype=torch.float32, device=dev)
+    ws = DenseDecodeWorkspace(B, H, L, dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        sparse_attention_decode_orchestrator(q, k, v, out, lens, None, alpha=a.alpha, niter=2,
+                                             workspace=ws, taus_out=taus)
+
+    ms = _time_loop(step, a.steps, a.warmup, stream)
+    # supported tokens at the final tau (the V rows the decode reads)
+    s = torch.einsum("bhd,bhld->bhl", q[:, :, 0].float(), k.float())
+    s = s * ((a.alpha - 1.0) / math.sqrt(D))
+    support = float((s > taus[..., None]).sum())
+    step_bytes = B * H * L * D * esz + support * D * esz + 2 * B * H * D * esz
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "dense decode-step us + effective KV GB/s (% HBM peak)",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
+        "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16 storage, f32 accumulate",
+        "data": "synthetic N(0,1) q/k/v, seed 1",
+        "config": {"workload": "dense entmax decode (sparse_attention_decode_orchestrator)",
+                   "batch": B, "heads": H, "head_dim": D, "kv_len": L, "alpha": a.alpha,
+                   "niter": 2, "mean_support": round(support / (B * H), 1),
+                   "bytes_per_step": step_bytes}}), flush=True)
+    return 0
+
+
+def _config_rows(a):
+    """Row-wise entmax forward and backward over 16384 rows of 8192 fp16
+    values (alpha 1.5).  Algorithmic bytes: forward reads x and writes y,
+    backward reads y and dy and writes dx."""
+    import torch
+
+    from entmaxkv_amd.entmax import entmax_backward, entmax_forward
+
+    R, N, esz = 16384, 8192, 2
+    dev = torch.device("cuda:0")
+    gd = torch.Generator(device=dev)
+    gd.manual_seed(2)
+    x = torch.randn(R, N, device=dev, dtype=torch.float16, generator=gd) * 3
+    dy = torch.randn(R, N, device=dev, dtype=torch.float16, generator=gd)
+    stream = torch.cuda.current_stream(dev)
+    y = entmax_forward(x, 1.5)
+    ms_f = _time_loop(lambda: entmax_forward(x, 1.5), a.steps, a.warmup, stream)
+    ms_b = _time_loop(lambda: entmax_backward(y, dy, 1.5), a.steps, a.warmup, stream)
+    fb, bb = 2.0 * R * N * esz, 3.0 * R * N * esz
+    gf, gb = fb / (ms_f * 1e-3) / 1e9, bb / (ms_b * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "row-wise entmax forward / backward GB/s (% HBM peak)",
+        "value": round(gf, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms_f, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16 storage, f32 accumulate",
+        "data": "synthetic N(0,9) x, N(0,1) dy, seed 2",
+        "forward": {"us": round(ms_f * 1e3, 2), "GBs": round(gf, 1),
+                    "pct_hbm_peak": round(100.0 * gf / HBM_PEAK_GBS, 2), "bytes": fb},
+        "backward": {"us": round(ms_b * 1e3, 2), "GBs": round(gb, 1),
+                     "pct_hbm_peak": round(100.0 * gb / HBM_PEAK_GBS, 2), "bytes": bb},
+        "config": {"workload": "triton_entmax rows", "rows": R, "n": N, "alpha": 1.5}}),
+        flush=True)
+    return 0
+
+
 def main():
     a = _args()
     if a.gpus != 1:
@@ -218,6 +302,10 @@ def main():
         return 2
     if a.config == "c5":
         return _config5(a)
+    if a.config == "dense":
+        return _config_dense(a)
+    if a.config == "rows":
+        return _config_rows(a)
     import numpy as np
     import torch
 

@@ -361,6 +361,10 @@ DenseGeom dense_geom(int B, int H, int64_t kv_rows) {
   return g;
 }
 
+// Heads longer than this are scored by many workgroups each (the split
+// path): one workgroup per head would stream all of its keys from one CU.
+constexpr int kDenseHeadTokens = 8192;
+
 __global__ void iota_kernel(int32_t* __restrict__ p, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = i;
@@ -396,6 +400,7 @@ extern "C" int ekv_dense_entmax_decode(
                       kv_rows, table, 0, 0, g.n_slots, cache_seqlens, 1, 0, q_seqlens,
                       alibi_slopes, nullptr, tau, 0, iters, out, out_stride_b, out_stride_h,
                       alpha, qscale, g.page_size, B, H, Hkv, D, splits_for(g.max_tokens),
-                      g.max_tokens, workspace, g.score_bytes, dtype, stream, false,
+                      g.max_tokens, workspace, g.score_bytes, dtype, stream,
+                      g.max_tokens > kDenseHeadTokens,
                       alibi_slopes ? token_positions : nullptr, pos_stride_b, pos_stride_h);
 }

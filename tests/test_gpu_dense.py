@@ -25,7 +25,9 @@ def _case(**kw):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("alpha", [1.5, 2.0, 1.25, 3.0])
-@pytest.mark.parametrize("n", [1, 7, 1000, 20000])
+# rows in registers (n <= 8192, 1..32 values per thread), in LDS (<= 16384)
+# and re-read from memory (longer)
+@pytest.mark.parametrize("n", [1, 7, 1000, 8192, 12000, 20000])
 def test_entmax_rows_forward(dtype, alpha, n):
     from entmaxkv_amd.entmax import entmax_forward
     _case(test="entmax_rows_forward", dtype=dtype, alpha=alpha, n=n)
@@ -56,11 +58,12 @@ def test_entmax_rows_forward(dtype, alpha, n):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("alpha", [1.5, 2.0, 1.25])
-def test_entmax_rows_backward_and_autograd(dtype, alpha):
+@pytest.mark.parametrize("n", [777, 4096, 10000])
+def test_entmax_rows_backward_and_autograd(dtype, alpha, n):
     from entmaxkv_amd import entmax as E
-    _case(test="entmax_rows_backward", dtype=dtype, alpha=alpha)
+    _case(test="entmax_rows_backward", dtype=dtype, alpha=alpha, n=n)
     rng = np.random.default_rng(7)
-    shape = (2, 3, 777)
+    shape = (2, 3, n)
     x = randn(rng, shape, dtype, 2.0)
     dy = randn(rng, shape, dtype)
     xt = to_dev(x, dtype).requires_grad_(True)
@@ -86,9 +89,13 @@ def test_entmax_convenience_names_and_strides():
     xt = to_dev(x, "fp32")
     y2 = triton_sparsemax(xt[:, :200])  # row stride 300, non-contiguous view
     y15 = triton_entmax15(xt.t().contiguous().t())  # column-major: copied to rows
+    # rows starting 4 bytes past a 16-byte boundary: element-wise loads
+    xw = randn(rng, (8, 2049), "fp16")
+    yu = triton_entmax15(to_dev(xw, "fp16")[:, 1:])
     torch.cuda.synchronize()
     assert_out_close(to_np(y2), O.entmax_rows(x[:, :200], 2.0), "fp32", "sparsemax")
     assert_out_close(to_np(y15), O.entmax_rows(x, 1.5), "fp32", "entmax15")
+    assert_out_close(to_np(yu), O.entmax_rows(xw[:, 1:], 1.5), "fp16", "unaligned")
 
 
 # ---------------------------------------------------------------------------
