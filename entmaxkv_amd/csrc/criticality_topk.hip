@@ -54,7 +54,7 @@ __global__ __launch_bounds__(kHeadThreads) void criticality_head_kernel(
     const float* __restrict__ slopes, T* __restrict__ scores, int H, int Hkv, int stride,
     int page_size, int seq_len, int q_pos, int k_sel, int last_page,
     const int32_t* __restrict__ seq_lens, int32_t* page_indices, int64_t pisb, int64_t pish,
-    int lds_key_cap) {
+    int lds_key_cap, int list_words) {
   extern __shared__ uint32_t lds_keys[];
   const int bkv = blockIdx.x;
   const int b = bkv / Hkv, kvh = bkv % Hkv;
@@ -71,7 +71,8 @@ __global__ __launch_bounds__(kHeadThreads) void criticality_head_kernel(
   topk_select_block<T, G, kHeadThreads>(sbase, stride, r.count, r.k, r.last_page,
                                         page_indices + b * pisb + kvh * pish, lds_keys,
                                         G > 1 ? lds_key_cap : (keep_keys ? r.count : 0),
-                                        keep_keys, nullptr, lds_keys + stride);
+                                        keep_keys, nullptr, lds_keys + stride, nullptr, 0,
+                                        list_words);
 }
 
 template <typename T, int LPR, int G>
@@ -134,7 +135,8 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const T* __restrict__ sc
                                                         int page_size,
                                                         const int32_t* __restrict__ seq_lens,
                                                         int32_t* page_indices, int64_t pisb,
-                                                        int64_t pish, int lds_key_cap) {
+                                                        int64_t pish, int lds_key_cap,
+                                                        int list_words) {
   const int bkv = blockIdx.x;
   const int b = bkv / Hkv, kvh = bkv % Hkv;
   const Ragged r = ragged_topk(seq_lens, b, page_size, stride, 0, 0, k, last_page);
@@ -142,21 +144,32 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const T* __restrict__ sc
   extern __shared__ uint32_t lds_keys[];
   topk_select_block<T, G, kThreads>(s0, stride, r.count, r.k, r.last_page,
                                     page_indices + b * pisb + kvh * pish, lds_keys, lds_key_cap,
-                                    false, nullptr, lds_keys + stride);
+                                    false, nullptr, lds_keys + stride, nullptr, 0, list_words);
 }
 
 // Dynamic LDS of the top-k select over `num_pages` pages: the staged keys
-// (G == 1, when they fit) or the page ranks plus one candidate list (G > 1,
-// required).  Returns the bytes (0: none) or -1 when a G > 1 select does not
-// fit; `cap` receives the key capacity.
-int64_t select_lds_bytes(int G, int num_pages, int k, int* cap) {
+// (G == 1, when they fit) or the page ranks plus the candidate lists (G > 1,
+// required: all G lists when they fit, else one).  Returns the bytes (0:
+// none) or -1 when a G > 1 select does not fit; `cap` receives the key
+// capacity and `list_words` the list words.
+int64_t select_lds_bytes(int G, int num_pages, int k, int* cap, int* list_words) {
+  *list_words = 0;
   if (G == 1) {
     *cap = num_pages <= kMaxStagedKeys ? num_pages : 0;
     return (int64_t)*cap * 4;
   }
   *cap = num_pages;
-  const int64_t bytes = ((int64_t)num_pages + group_list_words(G, k)) * 4;
-  return (num_pages <= kMaxStagedKeys && bytes <= kLdsPerWorkgroup - 8192) ? bytes : -1;
+  if (num_pages > kMaxStagedKeys) return -1;
+  // what the static LDS of these kernels leaves (their group histograms)
+  const int64_t limit = kLdsPerWorkgroup - 40960;
+  for (bool concurrent : {true, false}) {
+    const int64_t bytes = ((int64_t)num_pages + group_list_words(G, k, concurrent)) * 4;
+    if (bytes <= limit) {
+      *list_words = group_list_words(G, k, concurrent);
+      return bytes;
+    }
+  }
+  return -1;
 }
 
 int set_lds(const void* kern, int64_t bytes, const char* what) {
@@ -202,10 +215,10 @@ extern "C" int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q
       constexpr int LPR = decltype(lpr)::value;
       return dispatch_group(H / Hkv, [&](auto gv) {
         constexpr int G = decltype(gv)::value;
-        int cap = 0;
+        int cap = 0, list_words = 0;
         int64_t sel_lds = 0;
         if (k_select >= 0) {
-          sel_lds = select_lds_bytes(G, num_pages, k_select, &cap);
+          sel_lds = select_lds_bytes(G, num_pages, k_select, &cap, &list_words);
           EKV_REQUIRE(sel_lds >= 0,
                       "ekv_page_criticality: group top-k of %d of %d pages does not fit LDS",
                       k_select, num_pages);
@@ -220,7 +233,7 @@ extern "C" int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q
                              q_stride_b, q_stride_h, (const T*)kmin, (const T*)kmax, s_stride_b,
                              s_stride_h, s_stride_page, alibi_slopes, (T*)scores, H, Hkv, num_pages,
                              page_size, seq_len, q_pos, k_select, last_page, seq_lens,
-                             page_indices, pi_stride_b, pi_stride_h, cap);
+                             page_indices, pi_stride_b, pi_stride_h, cap, list_words);
           return check_launch("criticality_head_kernel");
         }
         // few heads: spread the pages of each head over many workgroups, then
@@ -238,7 +251,7 @@ extern "C" int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q
           if ((rc = set_lds((const void*)kern, sel_lds, "topk_kernel"))) return rc;
           hipLaunchKernelGGL(kern, dim3(B * Hkv), dim3(kThreads), (size_t)sel_lds, s,
                              (const T*)scores, H, Hkv, num_pages, k_select, last_page, page_size,
-                             seq_lens, page_indices, pi_stride_b, pi_stride_h, cap);
+                             seq_lens, page_indices, pi_stride_b, pi_stride_h, cap, list_words);
           return check_launch("topk_kernel");
         }
         return check_launch("criticality_kernel");
@@ -259,15 +272,15 @@ extern "C" int ekv_topk_pages(const void* scores, int B, int H, int Hkv, int num
     using T = decltype(tv);
     return dispatch_group(H / Hkv, [&](auto gv) {
       constexpr int G = decltype(gv)::value;
-      int cap = 0;
-      const int64_t sel_lds = select_lds_bytes(G, num_pages, k, &cap);
+      int cap = 0, list_words = 0;
+      const int64_t sel_lds = select_lds_bytes(G, num_pages, k, &cap, &list_words);
       EKV_REQUIRE(sel_lds >= 0, "ekv_topk_pages: group top-k of %d of %d pages does not fit LDS",
                   k, num_pages);
       auto kern = topk_kernel<T, G>;
       if (int rc = set_lds((const void*)kern, sel_lds, "topk_kernel")) return rc;
       hipLaunchKernelGGL(kern, dim3(B * Hkv), dim3(kThreads), (size_t)sel_lds, s,
                          (const T*)scores, H, Hkv, num_pages, k, last_page, 1, nullptr,
-                         page_indices, pi_stride_b, pi_stride_h, cap);
+                         page_indices, pi_stride_b, pi_stride_h, cap, list_words);
       return check_launch("topk_kernel");
     });
   });

@@ -30,9 +30,16 @@
 __device__ unsigned long long ekv_phase_timers[4096 * 16];
 #define EKV_STAMP(i) \
   if (threadIdx.x == 0 && blockIdx.x < 4096) ekv_phase_timers[blockIdx.x * 16 + (i)] = wall_clock64()
-// slot 6 in the top-k launch: the top-k threshold found (topk_device.h stamp 3)
-#define EKV_CSTAMP(i) \
-  if ((i) == 3) EKV_STAMP(6)
+// slot 6 in the top-k launch: the top-k threshold found (topk_device.h stamp
+// 3); slots 12-15: the group select's stages (stamps 12-15)
+#define EKV_CSTAMP(i)  \
+  do {                  \
+    if ((i) == 3) {     \
+      EKV_STAMP(6);     \
+    } else if ((i) >= 12) { \
+      EKV_STAMP(i);     \
+    }                   \
+  } while (0)
 #else
 #define EKV_STAMP(i)
 #endif
@@ -758,6 +765,7 @@ struct SelectArgs {
   int last_page;      // appended at slot k (the sentinel), or -1
   int key_cap;        // page keys that fit the dynamic LDS
   int head_keys;      // G > 1: every query head's page keys kept in LDS too
+  int list_words;     // G > 1: LDS words of the candidate lists
   const int32_t* seq_lens;  // [B] per-sequence lengths (ragged batch) or null
 };
 
@@ -787,9 +795,9 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
   const topk::Ragged r = topk::ragged_topk(t.seq_lens, b, a.page_size, t.num_pages, t.seq_len,
                                            t.q_pos, t.k, t.last_page);
   const bool keep = r.count <= t.key_cap;
-  // G > 1: [page ranks: num_pages][candidate list: 2k][head keys: G * num_pages]
+  // G > 1: [page ranks: num_pages][candidate lists: list_words][head keys: G * num_pages]
   uint32_t* list = keys + t.num_pages;
-  uint32_t* head_keys = G > 1 && t.head_keys ? list + topk::group_list_words(G, t.k) : nullptr;
+  uint32_t* head_keys = G > 1 && t.head_keys ? list + t.list_words : nullptr;
   EKV_STAMP(0);
   const T* sbase = topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC>(
       (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
@@ -800,7 +808,7 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
   int32_t* pi = const_cast<int32_t*>(a.page_indices) + b * a.pisb + kvh * a.pish;
   topk::topk_select_block<T, G, kHeadThreads>(sbase, t.num_pages, r.count, r.k, r.last_page, pi,
                                               keys, keep ? r.count : 0, keep, s_pages, list,
-                                              head_keys, t.num_pages);
+                                              head_keys, t.num_pages, t.list_words);
   __syncthreads();
   EKV_STAMP(2);
   const int n = token_count(a, b, kvh);

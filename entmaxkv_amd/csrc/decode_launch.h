@@ -68,19 +68,33 @@ int Launch<T, G>::topk(DecodeArgs a, SelectArgs t, int B, int Hkv, int D, int to
     auto kern = topk_decode_kernel<T, LPR, G, UC, UD>;
     const int64_t avail = lds_left((const void*)kern, "topk_decode_kernel");
     if (avail < 0) return EKV_ERR_HIP;
-    // keys (G == 1), or page ranks + candidate list (+ every head's keys when
-    // they fit, else the selection re-reads the scores) for G > 1; the decode
-    // scores reuse the same LDS afterwards
+    // keys (G == 1), or page ranks + candidate lists (all G at once when they
+    // fit, else one) + every head's keys when they fit (else the selection
+    // re-reads the scores) for G > 1; the decode scores reuse the same LDS
+    // afterwards.  The first layout that fits wins.
     const int64_t stage = (int64_t)tokens * G * 4;
-    const int64_t sel = ((int64_t)t.num_pages + topk::group_list_words(G, t.k)) * 4;
-    const int64_t sel_keys = sel + (G > 1 ? (int64_t)G * t.num_pages * 4 : 0);
     t.head_keys = 0;
-    int64_t lds = sel > stage ? sel : stage;
-    if (G > 1 && (sel_keys > stage ? sel_keys : stage) <= avail) {
-      t.head_keys = 1;
-      lds = sel_keys > stage ? sel_keys : stage;
+    t.list_words = 0;
+    int64_t lds = -1;
+    if (G == 1) {
+      const int64_t sel = (int64_t)t.num_pages * 4;
+      lds = sel > stage ? sel : stage;
+    } else {
+      for (int variant = 0; variant < 4 && lds < 0; ++variant) {
+        const bool concurrent = variant == 0 || variant == 2;
+        const bool keys_in_lds = variant < 2;
+        const int words = topk::group_list_words(G, t.k, concurrent);
+        int64_t sel = ((int64_t)t.num_pages + words) * 4;
+        if (keys_in_lds) sel += (int64_t)G * t.num_pages * 4;
+        const int64_t need = sel > stage ? sel : stage;
+        if (need <= avail) {
+          lds = need;
+          t.list_words = words;
+          t.head_keys = keys_in_lds ? 1 : 0;
+        }
+      }
     }
-    if (lds > avail) return EKV_OK;  // too big: the caller falls back
+    if (lds < 0 || lds > avail) return EKV_OK;  // too big: the caller falls back
     const int rc = set_dynamic_lds((const void*)kern, (size_t)lds, "topk_decode_kernel");
     if (rc) return rc;
     hipLaunchKernelGGL(kern, dim3(B * Hkv), dim3(kHeadThreads), (size_t)lds, s, a, t);

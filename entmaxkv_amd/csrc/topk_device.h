@@ -100,8 +100,10 @@ __device__ __forceinline__ void wave_hist_add(unsigned* hist, uint32_t bin, bool
 // one histogram per pass (LDS atomics), then every wave scans the 256 bins
 // itself (DPP prefix sum + ballot) to find the bin of the k-th largest key, so
 // a pass costs one barrier.  `hist` must be zero and visible to every thread
-// on entry.
-template <int NT, int kBits, typename KeyOf>
+// on entry.  Pass 0 adds through wave_hist_add (one atomic per distinct bin
+// per wave); later passes too when kAggregate (keys with many duplicates,
+// whose plain atomics would serialise on a few addresses).
+template <int NT, int kBits, typename KeyOf, bool kAggregate = false>
 __device__ __forceinline__ void radix_threshold(KeyOf key_of, int n, int k,
                                                 unsigned (*hist)[256], uint32_t& thr,
                                                 int& kk) {
@@ -126,9 +128,9 @@ __device__ __forceinline__ void radix_threshold(KeyOf key_of, int n, int k,
         const int p = p0 + j * NT + tid;
         const bool act = p < n && (kv[j] & pmask) == prefix;
         const uint32_t bin = (kv[j] >> shift) & 255u;
-        if (pass == 0) {
+        if (pass == 0 || kAggregate) {
           // wave-uniform: every lane takes part in the ballots
-          if (p0 + j * NT < n) wave_hist_add(hist[0], bin, act);
+          if (p0 + j * NT < n) wave_hist_add(hist[pass], bin, act);
         } else if (act) {
           atomicAdd(&hist[pass][bin], 1u);
         }
@@ -227,9 +229,153 @@ __device__ __forceinline__ void pack_selected(KeyOf key_of, int n, bool take_all
   }
 }
 
-// LDS words the select of a group of G query heads needs beyond the staged
-// keys: the candidate list of one head (page, key, rank) for G > 1.
-__host__ __device__ constexpr int group_list_words(int G, int k) { return G > 1 ? 3 * k : 0; }
+// Radix select of G key sets at once (query head g's keys key_of(g, p)): the
+// k-th largest key of each (thr[g]) and how many keys equal to it to take
+// (kk[g]).  One histogram per head per pass (hist[pass][g], zero and visible
+// on entry), one barrier per pass; every wave scans the G histograms itself.
+template <int NT, int kBits, int G, typename KeyOf>
+__device__ __forceinline__ void radix_threshold_group(KeyOf key_of, int n, int k,
+                                                      unsigned (*hist)[G][256],
+                                                      uint32_t (&thr)[G], int (&kk)[G]) {
+  constexpr int kPasses = kBits / 8;
+  constexpr int kBatch = 4;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  uint32_t prefix[G];
+  uint32_t pmask = 0;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    prefix[g] = 0;
+    kk[g] = k;
+  }
+#pragma unroll
+  for (int pass = 0; pass < kPasses; ++pass) {
+    const int shift = kBits - 8 * (pass + 1);
+    for (int p0 = 0; p0 < n; p0 += NT * kBatch) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        uint32_t kv[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int p = p0 + j * NT + tid;
+          kv[j] = p < n ? key_of(g, p) : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int p = p0 + j * NT + tid;
+          const bool act = p < n && (kv[j] & pmask) == prefix[g];
+          const uint32_t bin = (kv[j] >> shift) & 255u;
+          if (pass == 0) {
+            if (p0 + j * NT < n) wave_hist_add(hist[pass][g], bin, act);
+          } else if (act) {
+            atomicAdd(&hist[pass][g][bin], 1u);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    const int top = 255 - 4 * lane;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const unsigned* h = hist[pass][g];
+      const int c0 = (int)h[top], c1 = (int)h[top - 1];
+      const int c2 = (int)h[top - 2], c3 = (int)h[top - 3];
+      const int sum = c0 + c1 + c2 + c3;
+      const int incl = wave_incl_scan(sum);
+      const int excl = incl - sum;
+      const uint64_t hit = __ballot(excl < kk[g] && incl >= kk[g]);
+      const int src = (int)__builtin_ctzll(hit);
+      int e = excl, bin, rem;
+      if (e + c0 >= kk[g]) {
+        bin = top;
+        rem = kk[g] - e;
+      } else if ((e += c0) + c1 >= kk[g]) {
+        bin = top - 1;
+        rem = kk[g] - e;
+      } else if ((e += c1) + c2 >= kk[g]) {
+        bin = top - 2;
+        rem = kk[g] - e;
+      } else {
+        e += c2;
+        bin = top - 3;
+        rem = kk[g] - e;
+      }
+      bin = __builtin_amdgcn_readlane(bin, src);
+      rem = __builtin_amdgcn_readlane(rem, src);
+      prefix[g] |= ((uint32_t)bin) << shift;
+      kk[g] = rem;
+    }
+    pmask |= 255u << shift;
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) thr[g] = prefix[g];
+}
+
+// pack_selected for G key sets at once: emit(g, slot, p, key) for the pages
+// each head selects, ascending per head.  `wave_cnt` holds 2 * G * NT / 64
+// ints; one barrier.
+template <int NT, int G, typename KeyOf, typename Emit>
+__device__ __forceinline__ void pack_selected_group(KeyOf key_of, int n,
+                                                    const uint32_t (&thr)[G],
+                                                    const int (&kk)[G], int* wave_cnt,
+                                                    Emit emit) {
+  constexpr int W = NT / 64;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int per = (n + W - 1) / W;
+  const int pw0 = min(n, wid * per), pw1 = min(n, pw0 + per);
+  int gt_n[G], eq_n[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) gt_n[g] = eq_n[g] = 0;
+  for (int r0 = pw0; r0 < pw1; r0 += 64) {
+    const int p = r0 + lane;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const uint32_t key = p < pw1 ? key_of(g, p) : 0u;
+      gt_n[g] += __popcll(__ballot(p < pw1 && key > thr[g]));
+      eq_n[g] += __popcll(__ballot(p < pw1 && key == thr[g]));
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      wave_cnt[(g * W + wid) * 2] = gt_n[g];
+      wave_cnt[(g * W + wid) * 2 + 1] = eq_n[g];
+    }
+  }
+  __syncthreads();
+  int gt_base[G], eq_base[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    gt_base[g] = eq_base[g] = 0;
+    for (int w = 0; w < wid; ++w) {
+      gt_base[g] += wave_cnt[(g * W + w) * 2];
+      eq_base[g] += wave_cnt[(g * W + w) * 2 + 1];
+    }
+  }
+  for (int r0 = pw0; r0 < pw1; r0 += 64) {
+    const int p = r0 + lane;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const uint32_t key = p < pw1 ? key_of(g, p) : 0u;
+      const bool gt = p < pw1 && key > thr[g];
+      const bool eq = p < pw1 && key == thr[g];
+      const uint64_t mg = __ballot(gt), me = __ballot(eq);
+      const int gt_rank = gt_base[g] + __popcll(mg & below);
+      const int eq_rank = eq_base[g] + __popcll(me & below);
+      if (gt || (eq && eq_rank < kk[g])) emit(g, gt_rank + min(eq_rank, kk[g]), p, key);
+      gt_base[g] += __popcll(mg);
+      eq_base[g] += __popcll(me);
+    }
+  }
+}
+
+// LDS words of the candidate lists (page, key, rank) of a group of G > 1
+// query heads: all G lists at once (`concurrent`), else one list at a time.
+__host__ __device__ constexpr int group_list_words(int G, int k, bool concurrent = true) {
+  return G > 1 ? 3 * k * (concurrent ? G : 1) : 0;
+}
 
 // Block-wide top-k of one (b, kv head) over `num_pages` pages; writes
 // ascending page ids to out[0..k) (and lds_out[0..k) when non-null) and
@@ -243,14 +389,16 @@ __host__ __device__ constexpr int group_list_words(int G, int k) { return G > 1 
 //
 // G > 1 (the group shares one page table; no reference counterpart): pages
 // are taken by their best rank over the group's query heads, ties to the lower
-// page index -- round robin over the heads' own top-k lists.  Per head: a
-// radix select gives its top-k list (page, key) in `lds_list`, each entry's
-// rank within the list is counted (the list is ascending in page order, so
-// equal keys rank by page; every thread counts a slice of the list for one
-// entry), and `lds_keys` (num_pages words, required:
-// lds_cap >= num_pages) keeps each page's minimum rank.  Ranks become keys
-// k - rank and one more select takes the k best.  A head's keys come from
-// `head_keys[g * hk_stride + p]` when non-null, else from the scores.
+// page index -- round robin over the heads' own top-k lists.  Radix selects
+// give each head's top-k list (page, key) in `lds_list` -- all G heads in the
+// same passes when `list_words` >= group_list_words(G, k), else one head
+// after another -- each entry's rank within its list is counted (a list is
+// ascending in page order, so equal keys rank by page; every thread counts a
+// slice of one list for one entry), and `lds_keys` (num_pages words,
+// required: lds_cap >= num_pages) keeps each page's minimum rank.  Ranks
+// become keys k - rank and one more select takes the k best.  A head's keys
+// come from `head_keys[g * hk_stride + p]` when non-null, else from the
+// scores.
 template <typename T, int G, int NT = kThreads>
 __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int64_t head_stride,
                                                   int num_pages, int k, int last_page,
@@ -259,7 +407,7 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
                                                   int* lds_out = nullptr,
                                                   uint32_t* lds_list = nullptr,
                                                   const uint32_t* head_keys = nullptr,
-                                                  int hk_stride = 0) {
+                                                  int hk_stride = 0, int list_words = 0) {
   constexpr int W = NT / 64;
   constexpr int kBits = ScoreKey<T>::kBits;
   constexpr int kPasses = kBits / 8;
@@ -305,7 +453,70 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
     if (k > 0) pack_selected<NT>(key_of, num_pages, take_all, thr, kk, wave_cnt, emit_out);
   } else {
     uint32_t* level = lds_keys;
-    if (k > 0 && !take_all) {
+    // the final select runs on keys k - rank <= k <= 16384: one 8-bit pass
+    // when k < 256, else two; most pages share key 0, so every pass
+    // aggregates its adds
+    auto select_levels = [&](auto key_l, uint32_t& thr, int& kk) {
+      if (k < 256)
+        radix_threshold<NT, 8, decltype(key_l), true>(key_l, num_pages, k, hist, thr, kk);
+      else
+        radix_threshold<NT, 16, decltype(key_l), true>(key_l, num_pages, k, hist, thr, kk);
+    };
+    auto key_gp = [&](int g, int p) -> uint32_t {
+      return head_keys ? head_keys[g * hk_stride + p]
+                       : ScoreKey<T>::key(s0[g * head_stride + p]);
+    };
+    if (k > 0 && !take_all && list_words >= group_list_words(G, k)) {
+      __shared__ unsigned ghist[kPasses][G][256];
+      __shared__ int gwave_cnt[2 * G * W];
+      uint32_t* list_page = lds_list;              // [G][k]
+      uint32_t* list_key = lds_list + G * k;       // [G][k]
+      uint32_t* list_rank = lds_list + 2 * G * k;  // [G][k]
+      for (int p = tid; p < num_pages; p += NT) level[p] = (uint32_t)k;
+      for (int i = tid; i < kPasses * G * 256; i += NT) (&ghist[0][0][0])[i] = 0u;
+      for (int i = tid; i < G * k; i += NT) list_rank[i] = 0u;
+      __syncthreads();
+      uint32_t thr[G];
+      int kk[G];
+      radix_threshold_group<NT, kBits, G>(key_gp, num_pages, k, ghist, thr, kk);
+      EKV_CSTAMP(12);
+      pack_selected_group<NT, G>(key_gp, num_pages, thr, kk, gwave_cnt,
+                                 [&](int g, int slot, int p, uint32_t key) {
+                                   list_page[g * k + slot] = (uint32_t)p;
+                                   list_key[g * k + slot] = key;
+                                 });
+      __syncthreads();
+      EKV_CSTAMP(13);
+      // work item w: entry i of list g against slice s of that list
+      const int entries = G * k;
+      const int slices = entries < NT ? NT / entries : 1;
+      const int per = (k + slices - 1) / slices;
+      for (int w = tid; w < entries * slices; w += NT) {
+        const int e = w % entries, g = e / k, i = e % k;
+        const int j0 = (w / entries) * per, j1 = min(k, j0 + per);
+        const uint32_t* lk = list_key + g * k;
+        const uint32_t ki = lk[i];
+        uint32_t cnt = 0;
+        for (int j = j0; j < j1; ++j) {
+          const uint32_t kj = lk[j];
+          cnt += (kj > ki) | ((kj == ki) & (j < i));
+        }
+        if (cnt) atomicAdd(&list_rank[e], cnt);
+      }
+      __syncthreads();
+      for (int e = tid; e < entries; e += NT) atomicMin(&level[list_page[e]], list_rank[e]);
+      __syncthreads();
+      EKV_CSTAMP(14);
+      for (int p = tid; p < num_pages; p += NT) level[p] = (uint32_t)k - level[p];
+      zero_hist();
+      __syncthreads();
+      auto key_l = [&](int p) -> uint32_t { return level[p]; };
+      uint32_t thr1;
+      int kk1;
+      select_levels(key_l, thr1, kk1);
+      EKV_CSTAMP(15);
+      pack_selected<NT>(key_l, num_pages, false, thr1, kk1, wave_cnt, emit_out);
+    } else if (k > 0 && !take_all) {
       for (int p = tid; p < num_pages; p += NT) level[p] = (uint32_t)k;
       uint32_t* list_page = lds_list;
       uint32_t* list_key = lds_list + k;
@@ -314,10 +525,7 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
       const int per = (k + slices - 1) / slices;
 #pragma unroll 1
       for (int g = 0; g < G; ++g) {
-        auto key_g = [&](int p) -> uint32_t {
-          return head_keys ? head_keys[g * hk_stride + p]
-                           : ScoreKey<T>::key(s0[g * head_stride + p]);
-        };
+        auto key_g = [&](int p) -> uint32_t { return key_gp(g, p); };
         // the barrier also ends the previous head's use of the list
         zero_hist();
         for (int i = tid; i < k; i += NT) list_rank[i] = 0u;
@@ -351,11 +559,10 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
       for (int p = tid; p < num_pages; p += NT) level[p] = (uint32_t)k - level[p];
       zero_hist();
       __syncthreads();
-      // keys k - rank <= k <= 16384 fit 16 bits
       auto key_l = [&](int p) -> uint32_t { return level[p]; };
       uint32_t thr;
       int kk;
-      radix_threshold<NT, 16>(key_l, num_pages, k, hist, thr, kk);
+      select_levels(key_l, thr, kk);
       pack_selected<NT>(key_l, num_pages, false, thr, kk, wave_cnt, emit_out);
     } else if (k > 0) {
       pack_selected<NT>([](int) -> uint32_t { return 0u; }, num_pages, true, 0u, 0, wave_cnt,
