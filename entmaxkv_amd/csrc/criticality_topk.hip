@@ -260,6 +260,37 @@ extern "C" int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q
   });
 }
 
+// The criticality scores alone over many workgroups per (b, kv head)
+// (criticality_kernel), whatever the head count: the fused top-k step runs it
+// first when one workgroup per head would leave CUs idle.
+namespace ekv {
+namespace topk {
+int criticality_split_scores(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                             const void* kmin, const void* kmax, int64_t s_stride_b,
+                             int64_t s_stride_h, int64_t s_stride_page,
+                             const float* alibi_slopes, void* scores, int B, int H, int Hkv,
+                             int D, int num_pages, int page_size, int seq_len, int q_pos,
+                             const int32_t* seq_lens, int dtype, hipStream_t s) {
+  return dispatch_dtype(dtype, [&](auto tv) {
+    using T = decltype(tv);
+    return dispatch_lpr<T>(D, [&](auto lpr) {
+      constexpr int LPR = decltype(lpr)::value;
+      return dispatch_group(H / Hkv, [&](auto gv) {
+        constexpr int G = decltype(gv)::value;
+        constexpr int PPW = (kThreads / LPR) * kUnroll;
+        dim3 grid((num_pages + PPW - 1) / PPW, B * Hkv);
+        hipLaunchKernelGGL((criticality_kernel<T, LPR, G>), grid, dim3(kThreads), 0, s,
+                           (const T*)q, q_stride_b, q_stride_h, (const T*)kmin,
+                           (const T*)kmax, s_stride_b, s_stride_h, s_stride_page, alibi_slopes,
+                           (T*)scores, H, Hkv, num_pages, page_size, seq_len, q_pos, seq_lens);
+        return check_launch("criticality_kernel");
+      });
+    });
+  });
+}
+}  // namespace topk
+}  // namespace ekv
+
 extern "C" int ekv_topk_pages(const void* scores, int B, int H, int Hkv, int num_pages, int k,
                               int last_page, int32_t* page_indices, int64_t pi_stride_b,
                               int64_t pi_stride_h, int dtype, void* stream) {

@@ -766,12 +766,14 @@ struct SelectArgs {
   int key_cap;        // page keys that fit the dynamic LDS
   int head_keys;      // G > 1: every query head's page keys kept in LDS too
   int list_words;     // G > 1: LDS words of the candidate lists
+  int prescored;      // the scores are already in `scores` (a split scan ran first)
   const int32_t* seq_lens;  // [B] per-sequence lengths (ragged batch) or null
 };
 
-// One (b, kv head) per workgroup end to end: criticality scan of every page,
-// top-k (page table to global memory and to LDS), then phases 1-3 of the
-// decode on the selected pages.  Keys and then scores share the dynamic LDS.
+// One (b, kv head) per workgroup end to end: criticality scan of every page
+// (or, when t.prescored, the scores a split scan over every CU wrote), top-k
+// (page table to global memory and to LDS), then phases 1-3 of the decode on
+// the selected pages.  Keys and then scores share the dynamic LDS.
 template <typename T, int LPR, int G, int UC, int UD>
 __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a, SelectArgs t) {
   constexpr int VEC = 16 / sizeof(T);
@@ -799,15 +801,26 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
   uint32_t* list = keys + t.num_pages;
   uint32_t* head_keys = G > 1 && t.head_keys ? list + t.list_words : nullptr;
   EKV_STAMP(0);
-  const T* sbase = topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC>(
-      (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
-      a.slopes, (T*)t.scores, a.H, t.num_pages, r.count, a.page_size, r.seq_len, r.q_pos, b, kvh,
-      G == 1 ? (keep ? keys : nullptr) : head_keys);
+  const T* sbase = (const T*)t.scores + ((int64_t)b * a.H + kvh * G) * t.num_pages;
+  if (!t.prescored) {
+    topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC>(
+        (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
+        a.slopes, (T*)t.scores, a.H, t.num_pages, r.count, a.page_size, r.seq_len, r.q_pos, b,
+        kvh, G == 1 ? (keep ? keys : nullptr) : head_keys);
+  } else if (G > 1 && head_keys) {
+    // every query head's keys into LDS once (the select reads them per pass)
+    for (int i = threadIdx.x; i < G * r.count; i += kHeadThreads) {
+      const int g = i / r.count, p = i % r.count;
+      head_keys[g * t.num_pages + p] = topk::ScoreKey<T>::key(sbase[g * t.num_pages + p]);
+    }
+  }
   __syncthreads();
   EKV_STAMP(1);
   int32_t* pi = const_cast<int32_t*>(a.page_indices) + b * a.pisb + kvh * a.pish;
+  // G == 1: the scan left the keys in LDS; prescored, the select stages them
+  const bool staged = keep && !t.prescored;
   topk::topk_select_block<T, G, kHeadThreads>(sbase, t.num_pages, r.count, r.k, r.last_page, pi,
-                                              keys, keep ? r.count : 0, keep, s_pages, list,
+                                              keys, keep ? r.count : 0, staged, s_pages, list,
                                               head_keys, t.num_pages, t.list_words);
   __syncthreads();
   EKV_STAMP(2);

@@ -8,6 +8,17 @@
 using namespace ekv;
 using namespace ekv::dec;
 
+namespace ekv {
+namespace topk {
+int criticality_split_scores(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                             const void* kmin, const void* kmax, int64_t s_stride_b,
+                             int64_t s_stride_h, int64_t s_stride_page,
+                             const float* alibi_slopes, void* scores, int B, int H, int Hkv,
+                             int D, int num_pages, int page_size, int seq_len, int q_pos,
+                             const int32_t* seq_lens, int dtype, hipStream_t s);
+}  // namespace topk
+}  // namespace ekv
+
 namespace {
 
 template <typename F>
@@ -210,7 +221,19 @@ extern "C" int ekv_topk_paged_entmax_decode(
   t.last_page = last_page;
   t.key_cap = num_pages;
   t.seq_lens = seq_lens;
+  t.prescored = 0;
   hipStream_t s = (hipStream_t)stream;
+  // fewer (b, kv head) pairs than CUs: the criticality scan, the step's
+  // largest part, runs over every CU in a launch of its own, and the fused
+  // launch starts from its scores
+  if (B * Hkv < device_cus()) {
+    const int rc = topk::criticality_split_scores(
+        q, q_stride_b, q_stride_h, kmin, kmax, s_stride_b, s_stride_h, s_stride_page,
+        alibi_slopes, scores, B, H, Hkv, D, num_pages, page_size, seq_len, q_pos, nullptr, dtype,
+        s);
+    if (rc) return rc;
+    t.prescored = 1;
+  }
   int handled = 0;
   const int rc = dispatch_dtype(dtype, [&](auto tv) {
     using T = decltype(tv);

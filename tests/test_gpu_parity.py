@@ -174,8 +174,11 @@ def _decode_case(rng, dtype, B, Hkv, G, S, D, n_sel, k_scale=1.0):
 
 
 # "split": few heads, scores from a separate many-workgroup launch;
-# "head": batch * kv heads >= 128, one workgroup per (b, kv head) end to end.
-DECODE_SHAPES = {"split": (2, 2), "head": (8, 16)}
+# "head": batch * kv heads >= 128, one workgroup per (b, kv head) end to end
+# (the fused top-k step's scores come from a split scan first while batch * kv
+# heads is below the CU count); "wide": batch * kv heads = 256, the fused
+# top-k step scans in the same launch.
+DECODE_SHAPES = {"split": (2, 2), "head": (8, 16), "wide": (8, 32)}
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -305,7 +308,9 @@ def test_decode_edge_cases():
 TOPK_API_CASES = [("fp16", 1, "split", False), ("bf16", 4, "split", False),
                   ("fp32", 1, "split", False), ("fp16", 1, "head", False),
                   ("bf16", 4, "head", False), ("fp32", 2, "head", False),
-                  ("fp16", 1, "head", True), ("bf16", 8, "head", True)]
+                  ("fp16", 1, "head", True), ("bf16", 8, "head", True),
+                  ("fp16", 1, "wide", False), ("bf16", 4, "wide", True),
+                  ("fp32", 2, "wide", False)]
 
 
 @pytest.mark.parametrize("dtype,G,path,alibi", TOPK_API_CASES)
