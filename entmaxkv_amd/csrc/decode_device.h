@@ -169,8 +169,7 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
   constexpr int kNoRow = INT_MIN;
   // Rows of compacted tokens c0 + u * SEGS + seg and their K loads.  The loads
   // are unconditional (an invalid token re-reads row 0 and is masked), so
-  // all U of them are in flight together.  With explicit key positions the
-  // row is replaced by its position once the K load is issued.
+  // all U of them are in flight together.
   auto fetch = [&](int c0, int (&rows)[U], uint4 (&kv)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -184,11 +183,6 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) kv[u] = ld16(kh + (int64_t)max(rows[u], 0) * a.ksr + col);
-    if (kpos) {
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (rows[u] != kNoRow) rows[u] = kpos[rows[u]];
-    }
   };
   auto consume = [&](int c0, const int (&rows)[U], const uint4 (&kv)[U]) {
 #pragma unroll
@@ -201,9 +195,9 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
         if (c < c_end) {
           float s = acc;
           if (rows[u] == kNoRow) s = -INFINITY;
-          else if (a.slopes) s += slope[g] * (float)(rows[u] - q_idx);
+          else if (a.slopes && !kpos) s += slope[g] * (float)(rows[u] - q_idx);
           if (sl == 0) sc[g * stride + c] = s;
-          if (run_max) run_max[g] = fmaxf(run_max[g], s);
+          if (run_max && !kpos) run_max[g] = fmaxf(run_max[g], s);
         }
       }
     }
@@ -219,6 +213,24 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
     if (c0 + ROWS >= c_end) break;
     if (c0 + 2 * ROWS < c_end) fetch(c0 + 2 * ROWS, rows_a, kv_a);
     consume(c0 + ROWS, rows_b, kv_b);
+  }
+  if (kpos) {
+    // explicit key positions: the ALiBi term (and the running max) over the
+    // scores this lane wrote above; kept out of the scoring loop, whose K
+    // loads would otherwise all drain before every position load's use
+    for (int c = c_begin + seg; c < c_end; c += SEGS) {
+      const int page = pages[(c - c_base) / ps];
+      const int64_t row = (int64_t)page * ps + (c % ps);
+      const bool valid = page >= 0 && row < a.row_limit;
+      const float bias = valid ? (float)(kpos[valid ? row : 0] - q_idx) : 0.f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float s = sc[g * stride + c];
+        if (valid) s += slope[g] * bias;
+        if (sl == 0) sc[g * stride + c] = s;
+        if (run_max) run_max[g] = fmaxf(run_max[g], s);
+      }
+    }
   }
 }
 
