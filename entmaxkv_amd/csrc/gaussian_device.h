@@ -258,25 +258,38 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
   }
   const int p_begin = split * a.pages_per_split;
   const int p_end = min(pages, p_begin + a.pages_per_split);
-  float s_mu[G], s_mu2[G], s_var[G];
+  float s_mu[G], s_mu2[G], s_var[G], slope[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) s_mu[g] = s_mu2[g] = s_var[g] = 0.f;
+  for (int g = 0; g < G; ++g) {
+    s_mu[g] = s_mu2[g] = s_var[g] = 0.f;
+    slope[g] = a.slopes ? a.slopes[h0 + g] : 0.f;  // no load inside the scan loop
+  }
 
-  for (int p0 = p_begin; p0 < p_end; p0 += SEGS * U) {
-    // unconditional loads (a page past the end re-reads the last one, its
-    // result is discarded) so that all 2U loads are in flight together
-    VecRaw<T> mv[U], sv[U];
+  // Pages p0 + u * SEGS + seg: unconditional loads (a page past the end
+  // re-reads the last one, its result is discarded) so the compiler counts
+  // them exactly, in two register buffers: the next round's loads are issued
+  // (unconditionally: a conditional prefetch would make every consume wait
+  // for it) before the current round's arithmetic.
+  constexpr int ROUND = SEGS * U;
+  auto fetch = [&](int p0, VecRaw<T> (&mv)[U], VecRaw<T> (&sv)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int p = min(p0 + u * SEGS + seg, p_end - 1);
       mv[u].load(km + (int64_t)p * a.ssp + col);
       sv[u].load(ks + (int64_t)p * a.ssp + col);
     }
-    __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the arithmetic
+    __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the arithmetic
+  };
+  auto consume = [&](int p0, const VecRaw<T> (&mv)[U], const VecRaw<T> (&sv)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int p = p0 + u * SEGS + seg;
       const bool ok = p < p_end;
+      // a page past the end holds the last page's values (its loads were
+      // clamped): its stores rewrite them unchanged, so every lane stores
+      // unconditionally and the compiler keeps counting the loads exactly
+      const int pc = min(p, p_end - 1);
+      const bool acc = ok && sl == 0;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float mu = 0.f, var = 0.f;
@@ -288,22 +301,31 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
         }
         mu = seg_sum<LPR>(mu);
         var = seg_sum<LPR>(var);
-        if (ok && sl == 0) {
-          s_mu[g] += mu;
-          s_mu2[g] += mu * mu;
-          s_var[g] += var;
-          const int64_t o = ((int64_t)b * a.H + h0 + g) * a.pages + p;
-          float mub = mu;
-          if (a.slopes) {
-            // gaussian_utils.py:142-153: slope * (min(p*ps + (ps-1)/2, S'-1) - q_pos)
-            const float pos = fminf((float)p * (float)a.page_size + (float)(a.page_size - 1) * 0.5f,
-                                    (float)(stats_len - 1));
-            mub = add_rn(mu, mul_rn(a.slopes[h0 + g], sub_rn(pos, (float)q_pos)));
-          }
-          a.mu_p[o] = mub;
-          a.sigma_p[o] = sqrtf(var);
+        s_mu[g] += acc ? mu : 0.f;
+        s_mu2[g] += acc ? mu * mu : 0.f;
+        s_var[g] += acc ? var : 0.f;
+        const int64_t o = ((int64_t)b * a.H + h0 + g) * a.pages + pc;
+        float mub = mu;
+        if (a.slopes) {
+          // gaussian_utils.py:142-153: slope * (min(p*ps + (ps-1)/2, S'-1) - q_pos)
+          const float pos = fminf((float)pc * (float)a.page_size + (float)(a.page_size - 1) * 0.5f,
+                                  (float)(stats_len - 1));
+          mub = add_rn(mu, mul_rn(slope[g], sub_rn(pos, (float)q_pos)));
         }
+        a.mu_p[o] = mub;
+        a.sigma_p[o] = sqrtf(var);
       }
+    }
+  };
+  if (p_begin < p_end) {
+    VecRaw<T> mv_a[U], sv_a[U], mv_b[U], sv_b[U];
+    fetch(p_begin, mv_a, sv_a);
+    for (int p0 = p_begin; p0 < p_end; p0 += 2 * ROUND) {
+      fetch(p0 + ROUND, mv_b, sv_b);
+      consume(p0, mv_a, sv_a);
+      if (p0 + ROUND >= p_end) break;
+      fetch(p0 + 2 * ROUND, mv_a, sv_a);
+      consume(p0 + ROUND, mv_b, sv_b);
     }
   }
   // workgroup partials in a fixed order: lanes, then waves
