@@ -161,7 +161,7 @@ int64_t select_lds_bytes(int G, int num_pages, int k, int* cap, int* list_words)
   *cap = num_pages;
   if (num_pages > kMaxStagedKeys) return -1;
   // what the static LDS of these kernels leaves (their group histograms)
-  const int64_t limit = kLdsPerWorkgroup - 40960;
+  const int64_t limit = kLdsPerWorkgroup - kSelectStaticLds;
   for (bool concurrent : {true, false}) {
     const int64_t bytes = ((int64_t)num_pages + group_list_words(G, k, concurrent)) * 4;
     if (bytes <= limit) {
@@ -260,9 +260,7 @@ extern "C" int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q
   });
 }
 
-// The criticality scores alone over many workgroups per (b, kv head)
-// (criticality_kernel), whatever the head count: the fused top-k step runs it
-// first when one workgroup per head would leave CUs idle.
+// criticality_split_scores (declared in topk_device.h): criticality_kernel only.
 namespace ekv {
 namespace topk {
 int criticality_split_scores(const void* q, int64_t q_stride_b, int64_t q_stride_h,

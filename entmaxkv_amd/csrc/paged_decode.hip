@@ -8,17 +8,6 @@
 using namespace ekv;
 using namespace ekv::dec;
 
-namespace ekv {
-namespace topk {
-int criticality_split_scores(const void* q, int64_t q_stride_b, int64_t q_stride_h,
-                             const void* kmin, const void* kmax, int64_t s_stride_b,
-                             int64_t s_stride_h, int64_t s_stride_page,
-                             const float* alibi_slopes, void* scores, int B, int H, int Hkv,
-                             int D, int num_pages, int page_size, int seq_len, int q_pos,
-                             const int32_t* seq_lens, int dtype, hipStream_t s);
-}  // namespace topk
-}  // namespace ekv
-
 namespace {
 
 template <typename F>

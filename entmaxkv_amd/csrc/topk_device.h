@@ -19,6 +19,19 @@ constexpr int kUnroll = 4;  // pages per segment per workgroup
 // Page keys staged in LDS by the top-k pass (16384 pages = 256k tokens at
 // page size 16, 64 KB); longer caches re-read the scores on every pass.
 constexpr int kMaxStagedKeys = 16384;
+// Static LDS the top-k kernels of criticality_topk.hip may use (their group
+// histograms; 37 KB at fp32 and G = 8): the dynamic LDS sizing leaves it free.
+constexpr int kSelectStaticLds = 40960;
+
+// Host launcher (criticality_topk.hip) of the criticality scores alone over
+// many workgroups per (b, kv head), whatever the head count: the fused top-k
+// step runs it first when one workgroup per head would leave CUs idle.
+int criticality_split_scores(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                             const void* kmin, const void* kmax, int64_t s_stride_b,
+                             int64_t s_stride_h, int64_t s_stride_page,
+                             const float* alibi_slopes, void* scores, int B, int H, int Hkv,
+                             int D, int num_pages, int page_size, int seq_len, int q_pos,
+                             const int32_t* seq_lens, int dtype, hipStream_t s);
 
 // Top-k geometry of batch element b.  With per-sequence lengths, sequence b
 // scores its pages [0, P_b - 1) (the partial last page excluded), selects
