@@ -728,3 +728,42 @@ def test_gaussian_alibi_step(path):
     torch.cuda.synchronize()
     _check_gaussian_step(cache, q, k, v, out, dtype, G, "corrected", alpha, [S] * B,
                          slopes=slopes.astype(np.float64))
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (16, 8)])
+def test_topk_gqa_sequential_candidate_lists(shape):
+    """G = 8 with k = 2048 of 4096 pages: the group's candidate lists do not
+    fit LDS together, so the heads' selects run one after another (the split
+    top-k kernel for B * Hkv = 1; the one-workgroup-per-head criticality
+    kernel for 128, whose fused step does not fit one workgroup)."""
+    from entmaxkv_amd import sparse_attention_decode_paged
+    B, Hkv = shape
+    G, ps, D, dtype = 8, 16, 128, "bf16"
+    _case(test="topk_gqa_sequential", B=B, Hkv=Hkv, G=G)
+    rng = np.random.default_rng(77)
+    S0 = 16 * 4096
+    H = Hkv * G
+    cache, k, v = _build_cache(rng, B, Hkv, S0, D, dtype)
+    q = randn(rng, (B, H, 1, D), dtype)
+    kn = randn(rng, (B, Hkv, 1, D), dtype)
+    vn = randn(rng, (B, Hkv, 1, D), dtype)
+    S = S0 + 1
+    P = (S + ps - 1) // ps
+    budget = 2048 * ps
+    n_sel = min(budget // ps, P - 1)
+    out = torch.zeros(B, H, 1, D, dtype=TORCH_DT[dtype], device="cuda")
+    sparse_attention_decode_paged(
+        to_dev(q, dtype), cache, to_dev(kn, dtype), to_dev(vn, dtype), out, budget,
+        torch.full((B,), n_sel * ps + 1, dtype=torch.int32, device="cuda"),
+        torch.full((B,), S, dtype=torch.int32, device="cuda"), alpha=1.5, niter=10,
+        append_cache=True)
+    torch.cuda.synchronize()
+    sel = O.topk_gqa_pages(to_np(cache.last_page_scores), Hkv, n_sel)
+    pidx = np.concatenate([sel, np.full((B, Hkv, 1), P - 1)], axis=2)
+    np.testing.assert_array_equal(to_np(cache._page_indices_buf).astype(np.int64), pidx)
+    if B * Hkv == 1:
+        Kf = np.concatenate([k, kn], axis=2)
+        Vf = np.concatenate([v, vn], axis=2)
+        ref, _ = O.paged_entmax_decode(q[:, :, 0], Kf, Vf, pidx, np.full((B, Hkv), n_sel * ps + 1),
+                                       ps, 1.5, 10, dtype)
+        assert_out_close(to_np(out)[:, :, 0], ref, dtype)
