@@ -214,10 +214,12 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
     if (c0 + 2 * ROWS < c_end) fetch(c0 + 2 * ROWS, rows_a, kv_a);
     consume(c0 + ROWS, rows_b, kv_b);
   }
-  if (kpos) {
+  if (kpos && sl == 0) {
     // explicit key positions: the ALiBi term (and the running max) over the
-    // scores this lane wrote above; kept out of the scoring loop, whose K
-    // loads would otherwise all drain before every position load's use
+    // scores this lane wrote above (lane 0 of each row segment: it alone
+    // reads back its own stores); kept out of the scoring loop, whose K
+    // loads would otherwise all drain before every position load's use.  The
+    // running max is reduced over all lanes later, so lane 0 carries it.
     for (int c = c_begin + seg; c < c_end; c += SEGS) {
       const int page = pages[(c - c_base) / ps];
       const int64_t row = (int64_t)page * ps + (c % ps);
@@ -227,7 +229,7 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
       for (int g = 0; g < G; ++g) {
         float s = sc[g * stride + c];
         if (valid) s += slope[g] * bias;
-        if (sl == 0) sc[g * stride + c] = s;
+        sc[g * stride + c] = s;
         if (run_max) run_max[g] = fmaxf(run_max[g], s);
       }
     }
