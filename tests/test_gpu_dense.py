@@ -144,28 +144,38 @@ def test_dense_decode_matches_oracle(dtype, alpha, G, alibi, path):
     np.testing.assert_allclose(to_np(taus), ref_tau, atol=1e-4)
 
 
-def test_dense_decode_long_cache_and_profile():
-    """A cache longer than 2048 pages of 16 (the page grouping doubles) and the
-    profile dict."""
+@pytest.mark.parametrize("alibi", [False, True])
+def test_dense_decode_long_cache_and_profile(alibi):
+    """A cache longer than 2048 pages of 16 (the page grouping doubles; the
+    scores go through the workspace of the split scoring launch), with and
+    without explicit ALiBi positions, and the profile dict."""
     from entmaxkv_amd.kernels import sparse_attention_decode_orchestrator
-    _case(test="dense_decode_long")
+    _case(test="dense_decode_long", alibi=alibi)
     rng = np.random.default_rng(9)
     dtype, B, H, S, D = "bf16", 1, 2, 40000, 64
     K = randn(rng, (B, H, S, D), dtype)
     V = randn(rng, (B, H, S, D), dtype)
     q = randn(rng, (B, H, 1, D), dtype, 3.0)
     lens = np.array([S - 5])
+    slopes = np.array([0.01, 0.0005]) if alibi else None
+    pos = np.sort(rng.choice(2 * S, (B, H, S), replace=False), axis=-1) if alibi else None
+    q_sl = np.array([pos[0, :, : lens[0]].max() + 1]) if alibi else None
+    dev = lambda a: None if a is None else torch.tensor(a, device="cuda")
     out = torch.zeros(B, H, 1, D, dtype=TORCH_DT[dtype], device="cuda")
     prof = {}
     for _ in range(2):
         sparse_attention_decode_orchestrator(
             to_dev(q, dtype), to_dev(K, dtype), to_dev(V, dtype), out,
-            torch.tensor(lens, dtype=torch.int32, device="cuda"), None, alpha=1.5, niter=10,
-            profile=prof)
+            torch.tensor(lens, dtype=torch.int32, device="cuda"), dev(pos),
+            alibi_slopes=None if slopes is None else torch.tensor(slopes, dtype=torch.float32,
+                                                                  device="cuda"),
+            alpha=1.5, niter=10, q_seqlens=dev(q_sl), profile=prof)
     torch.cuda.synchronize()
-    ref, _ = O.dense_entmax_decode(q[:, :, 0], K, V, lens, 1.5, 10, dtype)
+    ref, _ = O.dense_entmax_decode(q[:, :, 0], K, V, lens, 1.5, 10, dtype, slopes, pos, q_sl)
     assert_out_close(to_np(out)[:, :, 0], ref, dtype)
     assert prof["_count"] == 2 and prof["total"] > 0.0
+    if alibi:
+        return
     # converged (10 steps): exact entmax over all keys
     qs = O.scaled_query(q[:, :, 0], 1.5, dtype)
     for h in range(H):
