@@ -20,11 +20,12 @@
 // Backward (kernels/triton_entmax.py:536-612): u = y^(2 - alpha) on the
 // support (1 for alpha = 2, sqrt(y) for 1.5), dx = u dy - (sum u dy / sum u) u.
 //
-// One workgroup of 256 threads per row.  Rows of up to 8192 elements stay in
-// registers (the next power of two of n / 256 per thread); longer rows keep z
-// in LDS when it fits (kRowCache floats), otherwise recompute it from x on
-// every pass.  Each pass ends in one block reduction of four values (one
-// barrier).
+// Workgroups of 256 threads, one row at a time.  Rows of up to 8192 elements
+// stay in registers (the next power of two of n / 256 per thread); longer
+// rows keep z in LDS when it fits (kRowCache floats), otherwise recompute it
+// from x on every pass.  Each pass ends in one block reduction of four values
+// (one barrier).  The forward of register rows read in 16-byte chunks runs
+// persistent workgroups that load their next row during the current one.
 #include "ekv_common.h"
 
 #include <initializer_list>
@@ -317,6 +318,55 @@ __global__ __launch_bounds__(kThreads) void entmax_fwd_kernel(const T* __restric
   if (tau_out && threadIdx.x == 0) tau_out[row] = t;
 }
 
+// Rows held in registers with 16-byte chunks, several rows per workgroup
+// (row blockIdx.x, then every gridDim.x-th): the next row's raw chunks are
+// loaded while the current row's tau is solved, so each CU keeps reading
+// while its workgroups sit in the reductions.  The grid holds as many
+// workgroups as fit on the device at once.
+template <typename T, int VPT, int E>
+__global__ __launch_bounds__(kThreads) void entmax_fwd_pipe_kernel(
+    const T* __restrict__ x, T* __restrict__ y, int64_t sx, int64_t sy, int n, float alpha,
+    float* __restrict__ tau_out, int rows) {
+  static_assert(E > 1 && VPT % E == 0, "16-byte chunks only");
+  constexpr int C = VPT / E;
+  __shared__ float4 rbuf[2][kWaves];
+  __shared__ unsigned hbin[2][kStartBins];
+  Reducer red{rbuf};
+  const float am1 = alpha - 1.0f;
+  VecRaw<T> nxt[C];
+  auto fetch = [&](int r) {
+    const T* xr = x + (int64_t)r * sx;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int i0 = (c * kThreads + (int)threadIdx.x) * E;
+      nxt[c].load(xr + min(i0, n - E));
+    }
+  };
+  int row = blockIdx.x;
+  if (row < rows) fetch(row);
+  for (int it = 0; row < rows; row += gridDim.x, ++it) {
+    // hbin[it & 1] was last read two rows ago, before at least one barrier
+    if (threadIdx.x < kStartBins) hbin[it & 1][threadIdx.x] = 0u;
+    RegVals<VPT, E> vals;
+    vals.n = n;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int i0 = (c * kThreads + (int)threadIdx.x) * E;
+#pragma unroll
+      for (int e = 0; e < E; ++e) vals.v[c * E + e] = i0 < n ? nxt[c].get(e) * am1 : -INFINITY;
+    }
+    if (row + (int)gridDim.x < rows) fetch(row + gridDim.x);
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) m = fmaxf(m, vals.v[j]);
+    m = -red.sum3_min(0.f, 0.f, 0.f, -m).w;  // its barrier publishes the zeroed bins
+    const float t = solve_row_tau(vals, n, m, alpha, red, hbin[it & 1]);
+    store_row<T, VPT, E>(y + (int64_t)row * sy, n,
+                         [&](int j) { return entmax_value(vals.v[j] - t, alpha); });
+    if (tau_out && threadIdx.x == 0) tau_out[row] = t;
+  }
+}
+
 __device__ __forceinline__ float entmax_grad_weight(float yv, float alpha) {
   if (!(yv > 0.f)) return 0.f;
   if (alpha == 2.0f) return 1.f;
@@ -365,6 +415,21 @@ __global__ __launch_bounds__(kThreads) void entmax_bwd_kernel(const T* __restric
       xr[i] = from_f<T>(uv * to_f<T>(gr[i]) - scalar * uv);
     }
   }
+}
+
+// Workgroups of a persistent row kernel: as many as are resident on the
+// device at once (occupancy per CU, queried once per kernel), at most `rows`.
+template <typename K>
+unsigned resident_grid(K kernel, int64_t rows) {
+  static int per_cu = -1;  // one per kernel instantiation; every device gets the same figure
+  if (per_cu < 0) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, kThreads, 0) != hipSuccess)
+      nb = 1;
+    per_cu = nb < 1 ? 1 : nb;
+  }
+  const int64_t slots = (int64_t)per_cu * device_cus();
+  return (unsigned)(rows < slots ? rows : slots);
 }
 
 // Registers per thread for a row of n: the next power of two of n / kThreads
@@ -422,10 +487,11 @@ extern "C" int ekv_entmax_rows_forward(const void* x, int64_t x_row_stride, void
       constexpr int EV = 16 / sizeof(T);
       if constexpr (VPT >= EV) {
         if (vec) {
-          hipLaunchKernelGGL((entmax_fwd_kernel<T, VPT, EV>), dim3((unsigned)rows),
-                             dim3(kThreads), lds, s, (const T*)x, (T*)y, x_row_stride,
-                             y_row_stride, n, alpha, tau_out);
-          return check_launch("entmax_fwd_kernel");
+          const unsigned grid = resident_grid(entmax_fwd_pipe_kernel<T, VPT, EV>, rows);
+          hipLaunchKernelGGL((entmax_fwd_pipe_kernel<T, VPT, EV>), dim3(grid), dim3(kThreads), 0,
+                             s, (const T*)x, (T*)y, x_row_stride, y_row_stride, n, alpha,
+                             tau_out, (int)rows);
+          return check_launch("entmax_fwd_pipe_kernel");
         }
       }
       hipLaunchKernelGGL((entmax_fwd_kernel<T, VPT, 1>), dim3((unsigned)rows), dim3(kThreads),

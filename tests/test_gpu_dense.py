@@ -57,6 +57,28 @@ def test_entmax_rows_forward(dtype, alpha, n):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("alpha", [1.5, 2.0])
+@pytest.mark.parametrize("n,rows", [(2048, 4200), (8192, 2100)])
+def test_entmax_rows_forward_many_rows(dtype, alpha, n, rows):
+    """More rows than resident workgroups: every workgroup of the register
+    path solves several rows, loading the next row during the current one."""
+    from entmaxkv_amd.entmax import entmax_forward
+    _case(test="entmax_rows_forward_many_rows", dtype=dtype, alpha=alpha, n=n, rows=rows)
+    rng = np.random.default_rng(rows + int(alpha * 10))
+    x = randn(rng, (rows, n), dtype, 3.0)
+    x[rows - 1, :5] = x[rows - 1, 0]  # ties in the last row
+    x[rows // 2] = x[rows // 2, 0]    # an all-equal row: uniform output
+    tau = torch.empty(rows, dtype=torch.float32, device="cuda")
+    y = entmax_forward(to_dev(x, dtype), alpha, tau_out=tau)
+    torch.cuda.synchronize()
+    z = (alpha - 1.0) * x
+    ref_tau = np.array([O.entmax_tau_exact(r, alpha) for r in z])
+    np.testing.assert_allclose(to_np(tau), ref_tau, atol=2e-6 * max(1.0, np.abs(ref_tau).max()))
+    assert_out_close(to_np(y), O.entmax_rows(x, alpha), dtype, "y")
+    np.testing.assert_allclose(to_np(y)[rows // 2], 1.0 / n, atol=ATOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("alpha", [1.5, 2.0, 1.25])
 @pytest.mark.parametrize("n", [777, 4096, 10000])
 def test_entmax_rows_backward_and_autograd(dtype, alpha, n):
@@ -79,6 +101,23 @@ def test_entmax_rows_backward_and_autograd(dtype, alpha, n):
     if dtype == "fp32":
         np.testing.assert_allclose(to_np(xt.grad), O.entmax_rows_backward(y_ref, dy, alpha),
                                    atol=1e-4)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n,rows", [(2048, 4200), (8192, 2100)])
+def test_entmax_rows_backward_many_rows(dtype, n, rows):
+    """More rows than resident workgroups in the backward's register path."""
+    from entmaxkv_amd import entmax as E
+    _case(test="entmax_rows_backward_many_rows", dtype=dtype, n=n, rows=rows)
+    rng = np.random.default_rng(rows)
+    x = randn(rng, (rows, n), dtype, 3.0)
+    dy = randn(rng, (rows, n), dtype)
+    xt = to_dev(x, dtype).requires_grad_(True)
+    y = E.triton_entmax(xt, alpha=1.5)
+    y.backward(to_dev(dy, dtype))
+    torch.cuda.synchronize()
+    ref = O.entmax_rows_backward(to_np(y), O.round_to(dy, dtype), 1.5)
+    assert_out_close(to_np(xt.grad), ref, dtype, "dx")
 
 
 def test_entmax_convenience_names_and_strides():
