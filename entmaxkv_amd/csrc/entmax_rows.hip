@@ -118,15 +118,16 @@ __device__ __forceinline__ void store_row(T* __restrict__ p, int n, F f) {
   }
 }
 
-// The row's z = (alpha - 1) x held in registers (see elem_index).
+// The row's z = (alpha - 1) x held in registers (see elem_index).  Slots
+// past the row's end hold -inf, which every pass skips (z - t > 0 fails), so
+// each() visits all slots without a range check.
 template <int VPT, int E>
 struct RegVals {
   float v[VPT];
   int n;
   template <typename F> __device__ __forceinline__ void each(F f) const {
 #pragma unroll
-    for (int j = 0; j < VPT; ++j)
-      if (elem_index<E>(j) < n) f(elem_index<E>(j), v[j]);
+    for (int j = 0; j < VPT; ++j) f(elem_index<E>(j), v[j]);
   }
 };
 
