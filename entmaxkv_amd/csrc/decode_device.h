@@ -54,6 +54,7 @@ namespace dec {
 
 constexpr int kSplitThreads = 256;
 constexpr int kSplitUnroll = 4;
+constexpr int kSplitTablePages = 1024;  // page ids staged in LDS per chunk of a split
 constexpr int kHeadThreads = 1024;
 constexpr int kWaves = kHeadThreads / 64;
 constexpr int kBins = 16;
@@ -533,8 +534,22 @@ __global__ __launch_bounds__(kSplitThreads) void score_split_kernel(DecodeArgs a
   if (c_start >= c_end) return;
   float* sc = a.ws_scores + ((int64_t)b * a.H + kvh * G) * a.max_tokens;
   const int32_t* pi = a.page_indices + b * a.pisb + kvh * a.pish;
-  score_rows<T, LPR, G, kSplitThreads, kSplitUnroll>(a, b, kvh, c_start, c_end, sc, a.max_tokens,
-                                                     pi, 0);
+  // The page ids come from LDS, a chunk at a time: read from global memory
+  // inside the loop, each one would wait behind the K loads already in flight
+  // (vector loads complete in order), which drains the second register buffer.
+  __shared__ int s_pages[kSplitTablePages];
+  const int ps = a.page_size;
+  for (int cb = c_start; cb < c_end;) {
+    const int p0 = cb / ps;
+    const int ce = min(c_end, (p0 + kSplitTablePages) * ps);
+    const int np = (ce - 1) / ps - p0 + 1;
+    __syncthreads();  // the previous chunk's readers are done
+    for (int i = threadIdx.x; i < np; i += kSplitThreads) s_pages[i] = pi[p0 + i];
+    __syncthreads();
+    score_rows<T, LPR, G, kSplitThreads, kSplitUnroll>(a, b, kvh, cb, ce, sc, a.max_tokens,
+                                                       (const int*)s_pages, p0 * ps);
+    cb = ce;
+  }
 }
 
 // ---------------------------------------------------------------------------
