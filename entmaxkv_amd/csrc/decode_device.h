@@ -667,15 +667,33 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
 #pragma unroll
     for (int i = 0; i < VEC; ++i) acc[g][i] = 0.f;
 
+  // The scores (and, from global memory, the page ids) of the next chunk of
+  // tokens are loaded before this chunk's V rows, so they have landed when
+  // the chunk after starts (the loads are clamped to the last token and
+  // issued unconditionally).
+  float s_nx[G];
+  int pg_nx = 0;
+  auto prefetch = [&](int t0) {
+    const int cc = min(t0 + tid, n - 1);
+#pragma unroll
+    for (int g = 0; g < G; ++g) s_nx[g] = sc[g * stride + cc];
+    if (!kTableInLds) pg_nx = pi[cc / ps];
+  };
+  if (n > 0) prefetch(0);
   for (int t0 = 0; t0 < n; t0 += kHeadThreads) {
     const int c = t0 + tid;
+    float s_cur[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) s_cur[g] = s_nx[g];
+    const int pg = pg_nx;
+    if (t0 + kHeadThreads < n) prefetch(t0 + kHeadThreads);
     float p[G];
     bool any = false;
     int64_t row = -1;
     if (c < n) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float s = sc[g * stride + c];
+        const float s = s_cur[g];
         p[g] = 0.f;
         if (s > tau[g]) {
           p[g] = entmax_weight(s - tau[g], alpha, c0);
@@ -683,7 +701,12 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
         }
       }
       if (any) {
-        row = token_row(kTableInLds ? sh.s_pages : pi, c, ps, a.row_limit);
+        if (kTableInLds) {
+          row = token_row(sh.s_pages, c, ps, a.row_limit);
+        } else {
+          const int64_t r = (int64_t)pg * ps + (c % ps);
+          row = (pg >= 0 && r < a.row_limit) ? r : -1;
+        }
         if (row < 0) any = false;
       }
     }
