@@ -532,16 +532,36 @@ __device__ __forceinline__ int select_pack_block(const SelectArgs& a, int b, int
   for (int g = 0; g < G; ++g) capmax[g] = -INFINITY;
   const int per = (pages + W - 1) / W;
   const int pw0 = min(pages, wid * per), pw1 = min(pages, pw0 + per);
+  // kSelBatch rounds of 64 pages per wave at a time: their loads are issued
+  // together (clamped to the wave's last page, unconditional), so a wave
+  // waits once per batch instead of once per round
+  constexpr int kSelBatch = 4;
   int cnt = 0;
-  for (int r0 = pw0; r0 < pw1; r0 += 64) {
-    const int p = r0 + lane;
-    const bool sel = p < pw1 && selected(p);
-    if (sel) {
+  for (int r0 = pw0; r0 < pw1; r0 += 64 * kSelBatch) {
+    float mv[kSelBatch][G], sv[kSelBatch][G];
+#pragma unroll
+    for (int u = 0; u < kSelBatch; ++u) {
+      const int pc = min(r0 + u * 64 + lane, pw1 - 1);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        mv[u][g] = mu[g][pc];
+        sv[u][g] = sg[g][pc];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSelBatch; ++u) {
+      bool sel = false;
 #pragma unroll
       for (int g = 0; g < G; ++g)
-        capmax[g] = fmaxf(capmax[g], fma_rn(mul_rn(a.z_clamp, sg[g][p]), third, mu[g][p]));
+        if (mul_rn(a.am1, fma_rn(z_page, sv[u][g], mv[u][g])) > tfloor[g]) sel = true;
+      sel = sel && r0 + u * 64 + lane < pw1;
+      if (sel) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          capmax[g] = fmaxf(capmax[g], fma_rn(mul_rn(a.z_clamp, sv[u][g]), third, mv[u][g]));
+      }
+      cnt += __popcll(__ballot(sel));
     }
-    cnt += __popcll(__ballot(sel));
   }
   if (lane == 0) wave_cnt[wid] = cnt;
 #pragma unroll
@@ -559,16 +579,22 @@ __device__ __forceinline__ int select_pack_block(const SelectArgs& a, int b, int
   }
   int32_t* out = a.page_indices + b * a.pisb + kvh * a.pish;
   const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  for (int r0 = pw0; r0 < pw1; r0 += 64) {
-    const int p = r0 + lane;
-    const bool sel = p < pw1 && selected(p);
-    const uint64_t m = __ballot(sel);
-    if (sel) {
-      const int slot = base + __popcll(m & below);
-      out[slot] = p;
-      if (slot < lds_cap) lds_pages[slot] = p;
+  for (int r0 = pw0; r0 < pw1; r0 += 64 * kSelBatch) {
+    bool selb[kSelBatch];
+#pragma unroll
+    for (int u = 0; u < kSelBatch; ++u) selb[u] = selected(min(r0 + u * 64 + lane, pw1 - 1));
+#pragma unroll
+    for (int u = 0; u < kSelBatch; ++u) {
+      const int p = r0 + u * 64 + lane;
+      const bool sel = selb[u] && p < pw1;
+      const uint64_t m = __ballot(sel);
+      if (sel) {
+        const int slot = base + __popcll(m & below);
+        out[slot] = p;
+        if (slot < lds_cap) lds_pages[slot] = p;
+      }
+      base += __popcll(m);
     }
-    base += __popcll(m);
   }
   int count = total;
   if (num_pages > pages) {
