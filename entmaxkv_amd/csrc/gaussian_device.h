@@ -32,12 +32,17 @@ namespace gauss {
 constexpr int moment_threads(int G) { return G <= 2 ? 1024 : 256; }
 
 // Workgroups per (b, kv head) of the moments launch: about 256K threads in
-// all, at least 256 pages each, at most 64 per head.
-inline int moment_splits(int bkv, int pages, int G) {
+// all, at least 256 pages each, at most 64 per head.  A ragged batch
+// (`ragged`: per-sequence lengths) takes 256 pages per workgroup of the
+// longest row whatever the thread count, so the long sequences do not leave
+// a few workgroups streaming long after the rest (a shorter sequence's extra
+// workgroups have no pages and exit).  Every launch that reads the partials
+// of one moments launch must pass the same `ragged`.
+inline int moment_splits(int bkv, int pages, int G, bool ragged = false) {
   const int target = (256 * 1024) / moment_threads(G);
   int s = (target + bkv - 1) / bkv;
   const int by_pages = (pages + 255) / 256;
-  if (s > by_pages) s = by_pages;
+  if (s > by_pages || ragged) s = by_pages;
   if (s > 64) s = 64;
   return s < 1 ? 1 : s;
 }

@@ -255,7 +255,7 @@ int ekv::gauss::launch_finalize(const void* partials, int B, int H, int Hkv, int
   const float lnf = (float)sqrt(2.0 * log((double)n_tokens + 1.0));
   hipLaunchKernelGGL(finalize_kernel, dim3((count + kThreads / 64 - 1) / (kThreads / 64)),
                      dim3(kThreads), 0, stream, (const float4*)partials,
-                     moment_splits(B * Hkv, pages, H / Hkv), pages, count, mu_g, sigma_g, mean_var,
+                     moment_splits(B * Hkv, pages, H / Hkv, seq_lens != nullptr), pages, count, mu_g, sigma_g, mean_var,
                      var_means, tau_hat, al, (float)n_tokens, lnf, tau_iters, tol, seq_lens,
                      page_size, H);
   return check_launch("finalize_kernel");
@@ -265,7 +265,8 @@ extern "C" int64_t ekv_gaussian_workspace_bytes(int B, int H, int Hkv, int D, in
   (void)D;
   (void)dtype;
   if (B <= 0 || H <= 0 || Hkv <= 0 || pages <= 0) return 0;
-  const int splits = moment_splits(B * Hkv, pages, H / Hkv);
+  // sized for the ragged split count, which is never below the uniform one
+  const int splits = moment_splits(B * Hkv, pages, H / Hkv, true);
   return ((int64_t)B * H * splits * 16 + 255) / 256 * 256;
 }
 
@@ -291,7 +292,7 @@ extern "C" int ekv_gaussian_moments(
   a.ssh = s_stride_h;
   a.ssp = s_stride_page;
   a.pages = pages_for_stats;
-  a.splits = moment_splits(B * Hkv, pages_for_stats, H / Hkv);
+  a.splits = moment_splits(B * Hkv, pages_for_stats, H / Hkv, seq_lens != nullptr);
   a.pages_per_split = (pages_for_stats + a.splits - 1) / a.splits;
   a.H = H;
   a.Hkv = Hkv;

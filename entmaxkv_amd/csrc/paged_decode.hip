@@ -328,7 +328,7 @@ extern "C" int ekv_gaussian_paged_entmax_decode(
   sel.eff = effective_margins;
   sel.seq_lens = seq_lens;
   f.partials = (const float4*)moments_workspace;
-  f.splits = gauss::moment_splits(B * Hkv, pages_for_stats, H / Hkv);
+  f.splits = gauss::moment_splits(B * Hkv, pages_for_stats, H / Hkv, seq_lens != nullptr);
   f.mu_g = mu_g;
   f.sigma_g = sigma_g;
   f.mean_var = mean_var;
