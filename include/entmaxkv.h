@@ -126,8 +126,10 @@ int64_t ekv_gaussian_workspace_bytes(int B, int H, int Hkv, int D, int pages, in
 /* Per-page score moments mu_p, sigma_p [B, H, pages_for_stats] (fp32, mu_p
  * with the ALiBi page-mean bias when alibi_slopes is non-null) and, in the
  * workspace, each workgroup's partial sums of the global moments: the first
- * launch of ekv_gaussian_page_stats and of the fused Gaussian step.
- * Replaces the moment kernel of compute_page_gaussian_stats_triton
+ * launch of ekv_gaussian_page_stats and of the fused Gaussian step.  The
+ * number of partials per head depends on whether seq_lens is given, so the
+ * decode call that reads this workspace must be given the same seq_lens
+ * (null or not).  Replaces the moment kernel of compute_page_gaussian_stats_triton
  * (kernels/gaussian_page_stats.py:8-121, 128-233). */
 int ekv_gaussian_moments(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kmean,
                          const void* kstd, int64_t s_stride_b, int64_t s_stride_h,
