@@ -223,13 +223,18 @@ struct MomentsArgs {
 //   sigma_p = sqrt(sum_d (q_d/sqrt(D))^2 std_pd^2),
 // and the workgroup's partial sums (of the unbiased mu_p).  A row segment of
 // LPR lanes owns a page; U pages per segment in flight.  blockDim == NT.
-template <typename T, int LPR, int G, int NT, int U>
+// Page moments of one workgroup staged in LDS (kLdsOut) before one coalesced
+// write-out per head after the scan, when pages_per_split * G fits.
+constexpr int kMomentLdsEntries = 4096;
+
+template <typename T, int LPR, int G, int NT, int U, bool kLdsOut = false>
 __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int b, int kvh,
                                                       int split) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int SEGS = NT / LPR;
   constexpr int W = NT / 64;
   __shared__ float4 red[G][W];
+  __shared__ float2 lds_out[kLdsOut ? kMomentLdsEntries : 1];
   const int seg = threadIdx.x / LPR;
   const int sl = threadIdx.x % LPR;
   const int col = sl * VEC;
@@ -317,8 +322,12 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
                                   (float)(stats_len - 1));
           mub = add_rn(mu, mul_rn(slope[g], sub_rn(pos, (float)q_pos)));
         }
-        a.mu_p[o] = mub;
-        a.sigma_p[o] = sqrtf(var);
+        if constexpr (kLdsOut) {
+          if (sl == 0) lds_out[(pc - p_begin) * G + g] = make_float2(mub, sqrtf(var));
+        } else {
+          a.mu_p[o] = mub;
+          a.sigma_p[o] = sqrtf(var);
+        }
       }
     }
   };
@@ -350,6 +359,19 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
       r.z += red[g][w].z;
     }
     a.partials[((int64_t)b * a.H + h0 + g) * a.splits + split] = r;
+  }
+  if constexpr (kLdsOut) {
+    // the barrier above also ordered every lds_out write before these reads
+    const int np = max(p_end - p_begin, 0);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t o = ((int64_t)b * a.H + h0 + g) * a.pages + p_begin;
+      for (int j = threadIdx.x; j < np; j += NT) {
+        const float2 v = lds_out[j * G + g];
+        a.mu_p[o + j] = v.x;
+        a.sigma_p[o + j] = v.y;
+      }
+    }
   }
 }
 

@@ -34,7 +34,11 @@ constexpr int kMomentUnroll = 2;
 template <typename T, int LPR, int G>
 __global__ __launch_bounds__(moment_threads(G)) void moments_kernel(MomentsArgs a) {
   const int bkv = blockIdx.y;
-  moments_partial_block<T, LPR, G, moment_threads(G), kMomentUnroll>(a, bkv / a.Hkv,
+  if (a.pages_per_split * G <= kMomentLdsEntries)
+    moments_partial_block<T, LPR, G, moment_threads(G), kMomentUnroll, true>(a, bkv / a.Hkv,
+                                                                           bkv % a.Hkv, blockIdx.x);
+  else
+    moments_partial_block<T, LPR, G, moment_threads(G), kMomentUnroll>(a, bkv / a.Hkv,
                                                                      bkv % a.Hkv, blockIdx.x);
 }
 
