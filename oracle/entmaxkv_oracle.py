@@ -286,6 +286,9 @@ def histogram_init(s: np.ndarray, alpha: float):
     init_tau_alpha2_tinit (:38-51), init_tau_alpha15_tinit (:54-71) and
     init_tau_generic_find_bin (:74-112).
     Returns (t, t_lo, t_hi, gmax, hist).
+    Pinned by: for scores on the bins' lower edges (and a unique maximum) the
+    alpha=2 and alpha=1.5 init equals the exact root (brentq); the truncation
+    quirk case; convergence of the iteration to exact entmax.
     """
     gmax = max(-1.0e6, float(np.max(s))) if s.size else -1.0e6
     t0 = gmax - 1.0
@@ -351,7 +354,11 @@ def histogram_init(s: np.ndarray, alpha: float):
 
 
 def entmax_accumulators(s: np.ndarray, t: float, alpha: float):
-    """(acc0, acc1, acc2) of kernels/adadecode_paged.py:357-372 at threshold t."""
+    """(acc0, acc1, acc2) of kernels/adadecode_paged.py:357-372 at threshold t.
+
+    Pinned by: f = acc0 - 1, f' = -acc1/(alpha-1) and f'' through the Halley
+    step checks (finite differences of the brute-force f).
+    """
     act = s - t
     m = act > 0
     a = act[m]
@@ -365,7 +372,12 @@ def entmax_accumulators(s: np.ndarray, t: float, alpha: float):
 
 
 def halley_bisect_update(t, t_lo, t_hi, acc0, acc1, acc2, alpha):
-    """Bracketed Halley step, kernels/adadecode.py:12-35 (EPS 1e-6)."""
+    """Bracketed Halley step, kernels/adadecode.py:12-35 (EPS 1e-6).
+
+    Pinned by: one step equals t - 2ff'/(2f'^2 - ff'') with f, f', f'' from
+    finite differences of the brute-force f; bracket update by sign(f); the
+    midpoint fallback; at alpha=2 one step lands on the sparsemax root.
+    """
     c0 = 1.0 / (alpha - 1.0)
     c1 = c0 - 1.0
     ff = acc0 - 1.0
@@ -456,7 +468,12 @@ def paged_entmax_decode(q, K, V, page_indices, cache_seqlens, page_size, alpha,
 
 
 def halley_unbounded_update(t, acc0, acc1, acc2, alpha):
-    """kernels/adadecode_paged_gaussian_tau.py:12-53 (Halley, else Newton, else keep)."""
+    """kernels/adadecode_paged_gaussian_tau.py:12-53 (Halley, else Newton, else keep).
+
+    Pinned by: one step equals textbook Halley on the brute-force f (finite
+    differences), alpha=1.5; lands exactly on the sparsemax root at alpha=2;
+    cubic error contraction near the root.
+    """
     c0 = 1.0 / (alpha - 1.0)
     c1 = c0 - 1.0
     ff = acc0 - 1.0

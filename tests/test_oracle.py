@@ -197,6 +197,161 @@ def test_generic_alpha_iteration():
 
 
 # ---------------------------------------------------------------------------
+# The single steps of the tau iteration the reference runs at small niter:
+# histogram init, one bracketed Halley step, one unbounded Halley step.  Each
+# is checked against f, f', f'' of sum_c [s_c - t]_+^(1/(alpha-1)) - 1 taken
+# by brute force and central finite differences, or against the exact root,
+# never against the oracle's own accumulators.
+# ---------------------------------------------------------------------------
+
+def _f_brute(s, t, alpha):
+    e = 1.0 / (alpha - 1.0)
+    return sum(max(x - t, 0.0) ** e for x in s) - 1.0
+
+
+def _f_derivs(s, t, alpha, h=1e-5):
+    """f, f' and f'' at t by central finite differences of the brute-force f.
+
+    With t at least h away from every score the support is fixed on [t-h, t+h],
+    where f is a polynomial of degree <= 2 for alpha in {1.5, 2}: the
+    differences are exact up to float64 rounding.
+    """
+    assert np.min(np.abs(np.asarray(s) - t)) > 4 * h
+    f0 = _f_brute(s, t, alpha)
+    fp = _f_brute(s, t + h, alpha)
+    fm = _f_brute(s, t - h, alpha)
+    return f0, (fp - fm) / (2 * h), (fp - 2 * f0 + fm) / (h * h)
+
+
+def _halley_textbook(t, f, d1, d2):
+    return t - 2.0 * f * d1 / (2.0 * d1 * d1 - f * d2)
+
+
+def _step_points(s, alpha, rng, count=6):
+    """Points t near the root, away from every score, with f(t) != 0."""
+    root = _bisect_tau(s, alpha)
+    pts = []
+    while len(pts) < count:
+        t = root + rng.uniform(-0.05, 0.05)
+        if np.min(np.abs(s - t)) > 1e-3 and abs(t - root) > 1e-4:
+            pts.append(t)
+    return root, pts
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_unbounded_halley_step_alpha15_is_textbook_halley(seed):
+    """kernels/adadecode_paged_gaussian_tau.py:12-53 at alpha=1.5: one step is
+    t - 2 f f' / (2 f'^2 - f f'') with f, f', f'' of the brute-force f."""
+    rng = np.random.default_rng(100 + seed)
+    s = rng.standard_normal(200) * 0.6
+    _, pts = _step_points(s, 1.5, rng)
+    for t in pts:
+        f, d1, d2 = _f_derivs(s, t, 1.5)
+        assert abs(d2) > 1e-3  # a Newton step would differ
+        want = _halley_textbook(t, f, d1, d2)
+        got = O.halley_unbounded_update(t, *O.entmax_accumulators(s, t, 1.5), 1.5)
+        assert abs(got - want) <= 1e-7 * max(1.0, abs(want)), (t, got, want)
+        newton = t - f / d1
+        assert abs(newton - want) > 1e2 * abs(got - want) + 1e-12
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_unbounded_halley_step_alpha2_lands_on_sparsemax_root(seed):
+    """At alpha=2, f is linear while the support stays fixed, so one unbounded
+    step from a point with the root's support lands exactly on the root."""
+    rng = np.random.default_rng(200 + seed)
+    s = rng.standard_normal(150) * 0.8
+    root = _bisect_tau(s, 2.0)
+    gap = np.min(np.abs(s - root))
+    above = s[s > root]
+    below = s[s <= root]
+    lo = max(root - 0.5 * gap, below.max() if below.size else -np.inf)
+    hi = min(root + 0.5 * gap, above.min())
+    for t in np.linspace(lo, hi, 7)[1:-1]:
+        if abs(t - root) < 1e-9:
+            continue
+        got = O.halley_unbounded_update(t, *O.entmax_accumulators(s, t, 2.0), 2.0)
+        assert abs(got - root) < 1e-12, (t, got, root)
+
+
+@pytest.mark.parametrize("alpha", [1.5, 2.0])
+def test_bracketed_halley_single_step(alpha):
+    """kernels/adadecode.py:12-35: bracket update by the sign of f, the Halley
+    point when it lies in the (updated) bracket widened by 1e-6, else the
+    midpoint."""
+    rng = np.random.default_rng(300)
+    s = rng.standard_normal(120) * 0.5
+    root, pts = _step_points(s, alpha, rng, count=8)
+    for t in pts:
+        f, d1, d2 = _f_derivs(s, t, alpha)
+        lo0, hi0 = root - 0.2, root + 0.2
+        got_t, got_lo, got_hi = O.halley_bisect_update(
+            t, lo0, hi0, *O.entmax_accumulators(s, t, alpha), alpha)
+        # f decreasing: f > 0 means t is left of the root
+        want_lo, want_hi = (t, hi0) if f > 0 else (lo0, t)
+        assert (got_lo, got_hi) == (want_lo, want_hi)
+        want = _halley_textbook(t, f, d1, d2)
+        assert want_lo - 1e-6 < want < want_hi + 1e-6
+        assert abs(got_t - want) <= 1e-7 * max(1.0, abs(want))
+        if alpha == 2.0 and np.min(np.abs(s - root)) > abs(t - root):
+            assert abs(got_t - root) < 1e-12
+    # a Halley point outside the bracket falls back to the bracket midpoint
+    t = root - 0.03
+    f, d1, d2 = _f_derivs(s, t, alpha)
+    lo0, hi0 = t - 1e-3, root - 0.02  # f(t) > 0 keeps hi0; the Halley point lands past it
+    got_t, got_lo, got_hi = O.halley_bisect_update(
+        t, lo0, hi0, *O.entmax_accumulators(s, t, alpha), alpha)
+    assert f > 0 and _halley_textbook(t, f, d1, d2) > hi0 + 1e-6
+    assert (got_lo, got_hi) == (t, hi0)
+    assert got_t == 0.5 * (t + hi0)
+
+
+def test_unbounded_halley_alpha15_cubic_convergence():
+    """Halley's error contracts cubically near a simple root: e1/e0^3 stays
+    bounded as e0 halves (Newton's would grow like 1/e0)."""
+    rng = np.random.default_rng(400)
+    s = rng.standard_normal(300) * 0.5
+    root = _bisect_tau(s, 1.5)
+    gap = np.min(np.abs(s - root))
+    ratios = []
+    for e0 in (gap / 4, gap / 8, gap / 16, gap / 32):
+        t = root + e0
+        t1 = O.halley_unbounded_update(t, *O.entmax_accumulators(s, t, 1.5), 1.5)
+        e1 = abs(t1 - root)
+        ratios.append(e1 / e0 ** 3)
+        assert e1 < e0 ** 2  # already better than a Newton step's scale
+    assert max(ratios) < 2.5 * min(ratios) + 1e-6, ratios
+
+
+def _edge_scores(rng, n, gmax=0.75):
+    """Scores sitting exactly on the lower edges of the 16 histogram bins of
+    s - (gmax - 1), plus the maximum itself (once: a second copy of the maximum
+    would be binned at z = 15/16); dyadic, so binning is exact."""
+    t0 = gmax - 1.0
+    js = rng.integers(0, 16, size=n)
+    return np.concatenate([[gmax], t0 + js / 16.0])
+
+
+@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("alpha", [2.0, 1.5])
+def test_histogram_init_exact_on_bin_edges(alpha, seed):
+    """kernels/adadecode.py:38-71: the alpha=2 and alpha=1.5 init treats every
+    binned score as sitting on its bin's lower edge and the maximum at z=1, so
+    for scores that sit exactly there it is the exact threshold (sparsemax /
+    entmax-1.5 closed form) of those scores, found here with brentq."""
+    rng = np.random.default_rng(500 + seed)
+    n = int(rng.integers(1, 40))
+    s = _edge_scores(rng, n)
+    if seed % 3 == 0:  # extra scores on the top bin's lower edge, beside the maximum
+        s = np.concatenate([s, [0.75 - 1.0 / 16] * 3])
+    t, t_lo, t_hi, gmax, hist = O.histogram_init(s, alpha)
+    assert gmax == 0.75 and hist.sum() == s.size
+    root = _bisect_tau(s, alpha)
+    assert abs(t_lo - root) < 1e-12, (t_lo, root)
+    assert t_hi == t_lo + 1.0 / 16 and t == 0.5 * (t_lo + t_hi)
+
+
+# ---------------------------------------------------------------------------
 # a7 Gaussian page stats
 # ---------------------------------------------------------------------------
 
