@@ -420,7 +420,7 @@ def main():
 
     cpu = None
     if not a.no_cpu_baseline:
-        cpu = _cpu_baseline(a, esz)
+        cpu = _cpu_baseline(a, esz, q, cache, step_bytes)
 
     value = step_bytes / (ms * 1e-3) / 1e9
     line = {
@@ -451,6 +451,7 @@ def main():
                      "avg_launch_us": round(ms * 1e3, 2), "bytes_per_launch": step_bytes},
         "gaussian": gauss,
         "cpu_baseline": cpu,
+        "build_id": _lib_build_id(),
     }
     headline = (B, H, Hkv, D, L, a.budget, a.dtype) == (8, 32, 32, 128, 32768, 1024, "fp16")
     traffic = _measured_traffic("topk_decode_kernel") if headline and fused else None
@@ -461,6 +462,11 @@ def main():
     return 0
 
 
+def _lib_build_id():
+    from entmaxkv_amd import _lib
+    return _lib.build_id()
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "topk_decode_kernel_pmc_b8h32l32k.md")
 
 
@@ -468,55 +474,77 @@ def _measured_traffic(kernel_tag):
     """HBM bytes per launch of the roofline kernel at the headline shape.
 
     Read from the committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE,
-    each scaled by the factor a copy kernel of known size gives); None when
-    the summary is absent or was taken on another kernel build.
+    each scaled by the factor a copy kernel of known size gives).  None unless
+    the summary names this kernel and the build id of the loaded library: a
+    figure taken on another build of the kernels is not reported.
     """
     import re
+
+    from entmaxkv_amd import _lib
     try:
         text = open(TRAFFIC_PROFILE).read()
     except OSError:
         return None
     k = re.search(r"^kernel:\s*(\S+)", text, re.M)
     m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
-    if not (k and m) or kernel_tag not in k.group(1):
+    b = re.search(r"^build_id:\s*(\S+)", text, re.M)
+    if not (k and m and b) or kernel_tag not in k.group(1) or b.group(1) != _lib.build_id():
         return None
     return int(m.group(1))
 
 
-def _cpu_baseline(a, esz):
-    """The oracle's top-k step on one batch element of the workload, on the host."""
-    import numpy as np
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    from oracle import entmaxkv_oracle as O
 
-    rng = np.random.default_rng(0)
-    H, D, L, ps = a.heads, a.head_dim, a.kv_len, 16
-    Hkv = a.kv_heads or H
-    S = L + 1
-    k = O.round_to(rng.standard_normal((1, Hkv, S, D)), a.dtype)
-    v = O.round_to(rng.standard_normal((1, Hkv, S, D)), a.dtype)
-    q = O.round_to(rng.standard_normal((1, H, D)), a.dtype)
-    from threadpoolctl import threadpool_limits
+def _cpu_threads():
+    """Host cores this process may use, at most 16 (the GPU box's CPU share
+    for one GPU, whatever the machine's core count is)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
 
-    st = O.page_stats(k, ps, a.dtype)  # not timed as part of the step below
+
+def _cpu_baseline(a, esz, q, cache, step_bytes):
+    """The top-k step restated in PyTorch on the host (float32, every usable
+    core), on the same cache contents as the GPU step: the full workload
+    (all B), timed over a bounded sample of about 10 s.  The cache tensors are
+    copied to host memory before the clock starts."""
+    import torch
+
+    from oracle import torch_cpu_step as T
+
+    if (a.kv_heads or a.heads) != a.heads:
+        return None  # the restatement is MHA only
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
+    qc = q[:, :, 0].float().cpu()
+    kc, vc = cache.k_cache.cpu(), cache.v_cache.cpu()
+    kmin, kmax = cache.k_min.cpu(), cache.k_max.cpu()
+    T.topk_decode_step(qc, kc, vc, kmin, kmax, a.budget, 16, a.alpha)  # warm-up
     reps = 0
-    with threadpool_limits(limits=1):  # one host core: BLAS runs single-threaded
-        t1 = time.perf_counter()
-        while True:  # a bounded sample: repeat the step for about 10 s
-            O.topk_decode_step(q, k, v, st, a.budget, ps, a.alpha, a.niter, a.dtype)
-            reps += 1
-            if time.perf_counter() - t1 >= 10.0:
-                break
-        t2 = t1 + (time.perf_counter() - t1) / reps
-    P = (S + ps - 1) // ps
-    n_sel = min(a.budget // ps, P - 1)
-    n_tok = n_sel * ps + (S - (P - 1) * ps)
-    bytes_ = Hkv * n_tok * D * esz * 2 + H * (P - 1) * D * esz + 2 * H * D * esz
-    return {"value": round(bytes_ / (t2 - t1) / 1e9, 4), "unit": "GB/s", "cores": 1,
-            "kind": "port", "sample": f"one batch element (B=1, H={H}, L={S}) of the workload, "
-                                      f"NumPy float64 oracle on one core (BLAS limited to 1 thread), {reps} "
-                                      f"steps in ~10 s, {t2 - t1:.3f} s per step",
-            "us_per_step": round((t2 - t1) * 1e6, 1)}
+    t1 = time.perf_counter()
+    while True:
+        T.topk_decode_step(qc, kc, vc, kmin, kmax, a.budget, 16, a.alpha)
+        reps += 1
+        if time.perf_counter() - t1 >= 10.0:
+            break
+    sec = (time.perf_counter() - t1) / reps
+    return {"value": round(step_bytes / sec / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"the full workload (B={a.batch}, H={a.heads}, L={a.kv_len + 1}), PyTorch "
+                      f"float32 restatement of the step (oracle/torch_cpu_step.py) with "
+                      f"torch.set_num_threads({threads}) on {_cpu_model()}; {reps} steps in "
+                      f"~10 s, {sec * 1e3:.1f} ms per step",
+            "us_per_step": round(sec * 1e6, 1), "cpu_model": _cpu_model()}
 
 
 if __name__ == "__main__":

@@ -27,6 +27,7 @@ F = ctypes.c_float
 SIGNATURES = {
     "ekv_last_error": (ctypes.c_char_p, []),
     "ekv_abi_version": (I, []),
+    "ekv_build_id": (ctypes.c_char_p, []),
     "ekv_page_stats": (I, [P, I64, I64, I64, P, P, P, P, I64, I64, I64, I, I, I, I, P, I, I, I, I,
                            P]),
     "ekv_append": (I, [P, P, I64, I64, P, P, I64, I64, I64, P, P, P, P, I64, I64, I64,
@@ -95,6 +96,11 @@ def lib():
             raise RuntimeError(f"entmaxkv_amd: library ABI {v}, expected {ABI_VERSION}; rebuild")
         _lib = handle
         return _lib
+
+
+def build_id() -> str:
+    """Source hash the loaded library was built from (ekv_build_id)."""
+    return lib().ekv_build_id().decode()
 
 
 def call(name: str, *args) -> None:

@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import glob
+import hashlib
 import os
 import subprocess
 
@@ -48,10 +49,25 @@ def _run(cmd):
                            f"{res.stdout}{res.stderr}")
 
 
+def build_id(srcs) -> str:
+    """First 16 hex digits of a SHA-256 over the sources, headers and flags."""
+    h = hashlib.sha256()
+    files = sorted(srcs) + sorted(glob.glob(os.path.join(CSRC, "*.h"))) + \
+        sorted(glob.glob(os.path.join(HERE, "..", "include", "*.h")))
+    for f in files:
+        h.update(os.path.basename(f).encode() + b"\0")
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    h.update(" ".join(CFLAGS).encode())
+    h.update(repr(INSTANCES).encode())
+    return h.hexdigest()[:16]
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     inc = ["-I", os.path.join(HERE, "..", "include")]
+    bid = build_id(srcs)
     objs, cmds = [], []
     for src in srcs:
         base = os.path.basename(src)
@@ -59,7 +75,8 @@ def build(verbose: bool = False) -> str:
         for tag, defs in variants:
             obj = os.path.join(OBJ, base + tag + ".o")
             objs.append(obj)
-            cmds.append([hipcc(), *CFLAGS, *defs, *inc, "-c", src, "-o", obj])
+            cmds.append([hipcc(), *CFLAGS, *defs, f'-DEKV_BUILD_ID="{bid}"', *inc, "-c", src,
+                         "-o", obj])
     workers = min(len(cmds), max(1, (os.cpu_count() or 2)))
     with cf.ThreadPoolExecutor(workers) as ex:
         for cmd, fut in zip(cmds, [ex.submit(_run, c) for c in cmds]):

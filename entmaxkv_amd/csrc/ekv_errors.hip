@@ -47,3 +47,9 @@ int check_launch(const char* what) {
 extern "C" const char* ekv_last_error(void) { return g_err; }
 
 extern "C" int ekv_abi_version(void) { return EKV_ABI_VERSION; }
+
+#ifndef EKV_BUILD_ID
+#define EKV_BUILD_ID "unknown"
+#endif
+
+extern "C" const char* ekv_build_id(void) { return EKV_BUILD_ID; }

@@ -34,6 +34,11 @@ extern "C" {
 
 const char* ekv_last_error(void);
 int ekv_abi_version(void);
+/* Source hash of this build: the first 16 hex digits of a SHA-256 over the
+ * library's sources, this header and the compile flags (written by the build
+ * script).  Profiles record it, so that a measurement can be tied to the
+ * library that produced it.  No counterpart in the reference. */
+const char* ekv_build_id(void);
 
 /* Per-page key statistics over pages [page_begin, page_end): min, max, mean and
  * population std (clamped >= 1e-6) of rows [p*ps, min((p+1)*ps, seq_len)).

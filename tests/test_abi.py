@@ -56,3 +56,23 @@ def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "nope.so"))
     with pytest.raises(RuntimeError):
         _lib.lib()
+
+
+def test_integration_snippet_matches_the_abi():
+    """The reference-side ctypes block of INTEGRATION.md declares, and passes,
+    exactly the parameters of ekv_page_criticality."""
+    import ast
+    import ctypes
+
+    from entmaxkv_amd import _lib
+    from integration_snippet import load_snippet, snippet_source
+
+    mod = load_snippet(_lib.LIB_PATH)
+    argtypes = mod._lib.ekv_page_criticality.argtypes
+    want = _lib.SIGNATURES["ekv_page_criticality"][1]
+    assert len(argtypes) == _declared()["ekv_page_criticality"] == len(want)
+    for i, (a, b) in enumerate(zip(argtypes, want)):
+        assert a is b, (i, a, b)
+    calls = [n for n in ast.walk(ast.parse(snippet_source()))
+             if isinstance(n, ast.Call) and getattr(n.func, "attr", "") == "ekv_page_criticality"]
+    assert len(calls) == 1 and len(calls[0].args) == len(argtypes)

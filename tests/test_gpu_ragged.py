@@ -122,16 +122,19 @@ def test_ragged_topk_step(path, G, dtype):
 
 
 # config 5 in miniature: GQA, Gaussian alpha 1.5, append_cache=True, several
-# consecutive steps; "head" = one fused launch per step, "split" = few heads
-@pytest.mark.parametrize("path,G,tau_mode", [("head", 4, "corrected"), ("head", 1, "exact"),
-                                             ("split", 2, "corrected")])
-def test_ragged_gaussian_steps(path, G, tau_mode):
+# consecutive steps; "head" = one fused launch per step, "split" = few heads.
+# D = 128 with G = 4 in bf16 is config 5's own head shape.
+@pytest.mark.parametrize("path,G,tau_mode,D", [("head", 4, "corrected", 64), ("head", 1, "exact", 64),
+                                               ("split", 2, "corrected", 64),
+                                               ("head", 4, "corrected", 128),
+                                               ("split", 4, "corrected", 128)])
+def test_ragged_gaussian_steps(path, G, tau_mode, D):
     from entmaxkv_amd import sparse_attention_decode_gaussian_aware_entmax
-    _case(test="ragged_gaussian", path=path, G=G, tau_mode=tau_mode)
+    _case(test="ragged_gaussian", path=path, G=G, tau_mode=tau_mode, D=D)
     dtype, alpha = "bf16", 1.5
     rng = np.random.default_rng(81 + G)
     B, Hkv = (8, 16) if path == "head" else (3, 2)
-    S, D = 16 * 90, 64
+    S = 16 * 90
     H = Hkv * G
     q, k, v = _gqa_gaussian_inputs(rng, dtype, B, Hkv, G, S, D, 0.03)
     lens = [int(x) for x in rng.integers(40, S - 3, B)]

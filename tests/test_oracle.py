@@ -720,3 +720,28 @@ def test_gqa_topk_policy_accuracy_vs_dense():
                 errs_rank.append(er)
                 errs_max.append(em)
     assert np.mean(errs_rank) < 0.5 * np.mean(errs_max), (errs_rank, errs_max)
+
+
+# ---------------------------------------------------------------------------
+# the PyTorch-CPU restatement the benchmark times as its CPU baseline
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("alpha", [1.5, 2.0])
+def test_torch_cpu_step_matches_oracle(alpha):
+    from oracle import torch_cpu_step as T
+
+    rng = np.random.default_rng(9)
+    B, H, S, D, ps, budget = 2, 3, 16 * 40 + 7, 32, 16, 160
+    k = O.round_to(rng.standard_normal((B, H, S, D)), "fp32")
+    v = O.round_to(rng.standard_normal((B, H, S, D)), "fp32")
+    q = O.round_to(rng.standard_normal((B, H, D)), "fp32")
+    st = O.page_stats(k, ps, "fp32")
+    ref, _, _ = O.topk_decode_step(q, k, v, st, budget, ps, alpha, 40, "fp32")
+    t = lambda x: torch.tensor(x, dtype=torch.float32)
+    got = T.topk_decode_step(t(q), t(k), t(v), t(st[0]), t(st[1]), budget, ps, alpha)
+    np.testing.assert_allclose(got.double().numpy(), ref, atol=2e-5)
+    # the sorted-threshold helper against brentq on random rows
+    s = rng.standard_normal((4, 300)) * 0.7
+    taus = T.entmax_tau_sorted(torch.tensor(s), alpha).numpy()
+    for i in range(4):
+        assert abs(taus[i] - _bisect_tau(s[i], alpha)) < 1e-9
