@@ -43,6 +43,10 @@ SIGNATURES = {
                                          I64, I64, I64, I64, P, I64, I64, P, I64, I64, P, P, P,
                                          P, I, P, I64, I64, F, F, I, I, I, I, I, I, I, P, I64,
                                          I, P]),
+    "ekv_topk_paged_entmax_decode_noalloc": (I, [P, I64, I64, P, P, I64, I64, I64, P, I, I, I,
+                                                 I, I, P, P, I64, I64, I64, I64, P, I64, I64, P,
+                                                 I64, I64, P, P, P, P, I, P, I64, I64, F, F, I,
+                                                 I, I, I, I, I, I, I, P]),
     "ekv_gaussian_workspace_bytes": (I64, [I, I, I, I, I, I]),
     "ekv_gaussian_page_stats": (I, [P, I64, I64, P, P, I64, I64, I64, I, P, I, I, P, P, P, P, P,
                                     P, P, F, I, I, F, P, I, I, I, I, P, I64, I, P]),

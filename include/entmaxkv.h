@@ -124,6 +124,31 @@ int ekv_topk_paged_entmax_decode(
     int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens, void* workspace,
     int64_t workspace_bytes, int dtype, void* stream);
 
+/* Size of the static device scratch of ekv_topk_paged_entmax_decode_noalloc. */
+#define EKV_NOALLOC_SCRATCH_BYTES (16ll << 20)
+
+/* ekv_topk_paged_entmax_decode without the workspace arguments: it calls no
+ * allocator.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under hipGraph capture, serving loops that
+ * forbid hipMalloc).  The workspace is a static device array of
+ * EKV_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a step
+ * whose workspace (ekv_decode_workspace_bytes: B * H * max_tokens * 4 bytes)
+ * exceeds it is rejected with EKV_ERR_ARG and nothing is launched.  Every
+ * call on one GPU shares that GPU's array, so calls that overlap on one GPU
+ * (other streams, other host threads) race and must be serialised by the
+ * caller.  Results equal ekv_topk_paged_entmax_decode's. */
+int ekv_topk_paged_entmax_decode_noalloc(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kmin, const void* kmax,
+    int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, void* scores, int num_pages,
+    int seq_len, int q_pos, int k_select, int last_page, const void* k, const void* v,
+    int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+    int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h,
+    const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
+    const int32_t* q_seqlens, const float* alibi_slopes, const int32_t* seq_lens, float* tau,
+    int niter, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale,
+    int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens, int dtype,
+    void* stream);
+
 /* Workspace for ekv_gaussian_moments / ekv_gaussian_page_stats (the partial
  * sums of the global moments; needs no initialisation). */
 int64_t ekv_gaussian_workspace_bytes(int B, int H, int Hkv, int D, int pages, int dtype);
