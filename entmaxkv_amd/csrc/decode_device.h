@@ -59,11 +59,9 @@ constexpr int kHeadThreads = 1024;
 constexpr int kWaves = kHeadThreads / 64;
 constexpr int kBins = 16;
 constexpr int kBatch = 8;           // independent loads per lane in score passes
-#ifndef EKV_WAVE_TAU_MAX
-#define EKV_WAVE_TAU_MAX 4096
-#endif
-constexpr int kWaveTauMax = EKV_WAVE_TAU_MAX;   // longer token lists solve tau with the whole workgroup
 constexpr int kTablePages = 2048;   // page ids staged in LDS per phase-1 chunk
+// tokens whose support the V phase compacts at once (two per thread for G <= 2)
+__host__ __device__ constexpr int sup_chunk(int G) { return G <= 2 ? 2 * kHeadThreads : kHeadThreads; }
 
 struct DecodeArgs {
   const void* q;
@@ -242,22 +240,9 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
 // kernels/adadecode_paged_gaussian_tau.py:12-53
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ void histogram_init(const int* hist, float gmax, float alpha, float& t, float& t_lo,
-                               float& t_hi) {
+__device__ __forceinline__ void histogram_init_vals(const int (&hv)[kBins], float gmax, float alpha,
+                                                    float& t, float& t_lo, float& t_hi) {
   const float t0 = gmax - 1.0f;
-  // all bins in registers first (one LDS round trip instead of one per bin)
-  int hv[kBins];
-  {
-    const int4* h4 = reinterpret_cast<const int4*>(hist);
-#pragma unroll
-    for (int j = 0; j < kBins / 4; ++j) {
-      const int4 x = h4[j];
-      hv[4 * j] = x.x;
-      hv[4 * j + 1] = x.y;
-      hv[4 * j + 2] = x.z;
-      hv[4 * j + 3] = x.w;
-    }
-  }
   if (alpha == 2.0f || alpha == 1.5f) {
     float sum_z = 1.f, sum_k = 1.f, sum_z2 = 1.f;
 #pragma unroll
@@ -324,6 +309,71 @@ __device__ __forceinline__ void histogram_init(const int* hist, float gmax, floa
     t_lo = t0 + (float)b_sel / kBins;
     t_hi = t0 + (float)min(b_sel + 1, kBins) / kBins;
   }
+  t = 0.5f * (t_lo + t_hi);
+}
+
+__device__ __forceinline__ void histogram_init(const int* hist, float gmax, float alpha, float& t,
+                                               float& t_lo, float& t_hi) {
+  // all bins in registers first (one LDS round trip instead of one per bin)
+  int hv[kBins];
+  const int4* h4 = reinterpret_cast<const int4*>(hist);
+#pragma unroll
+  for (int j = 0; j < kBins / 4; ++j) {
+    const int4 x = h4[j];
+    hv[4 * j] = x.x;
+    hv[4 * j + 1] = x.y;
+    hv[4 * j + 2] = x.z;
+    hv[4 * j + 3] = x.w;
+  }
+  histogram_init_vals(hv, gmax, alpha, t, t_lo, t_hi);
+}
+
+// Token counts up to which the bin sums of histogram_init_wave are exact in
+// fp32 (sum of count * bin^2 below 2^24).
+constexpr int kExactInitTokens = 65536;
+
+// histogram_init over bin counts that lane j (j < kBins) of the wave holds
+// for bin kBins - 1 - j, alpha 2 and 1.5 only: every lane takes the suffix
+// sums of the bins from the top down to its own (exact integer prefix sums
+// scaled by 1/16 and 1/256, so every sum and every test below is exact in
+// fp32 for the token counts of this path and equals the serial loop of
+// histogram_init), the accepted bins are the top run whose test holds (the
+// test is monotone in the bin), and the sums of its lowest bin give t.
+__device__ __forceinline__ void histogram_init_wave(int cnt_rev, float gmax, float alpha,
+                                                    float& t, float& t_lo, float& t_hi) {
+  const int lane = threadIdx.x & 63;
+  const int sj = kBins - 1 - lane;  // this lane's bin
+  const int c = lane < kBins ? cnt_rev - (lane == 0 ? 1 : 0) : 0;
+  const int ik = wave_incl_scan(c);
+  const int iz = wave_incl_scan(c * sj);
+  const int iz2 = wave_incl_scan(c * sj * sj);
+  const float c_tau = (float)sj / (float)kBins;
+  const float new_z = 1.0f + (float)iz / (float)kBins;
+  const float new_k = 1.0f + (float)ik;
+  const float new_z2 = 1.0f + (float)iz2 / (float)(kBins * kBins);
+  bool ok;
+  if (alpha == 2.0f) {
+    ok = (new_z - new_k * c_tau) < 1.0f;
+  } else {
+    ok = new_k * c_tau * c_tau - 2.0f * new_z * c_tau + new_z2 < 1.0f;
+  }
+  const uint64_t acc = __ballot(lane < kBins && ok);
+  const int m = (int)__builtin_ctzll(~acc);  // accepted bins: lanes 0 .. m-1
+  float sum_z = 1.f, sum_k = 1.f, sum_z2 = 1.f;
+  if (m > 0) {
+    sum_z = __shfl(new_z, m - 1);
+    sum_k = __shfl(new_k, m - 1);
+    sum_z2 = __shfl(new_z2, m - 1);
+  }
+  float t_init;
+  if (alpha == 2.0f) {
+    t_init = gmax + (sum_z - 1.0f) / sum_k - 1.0f;
+  } else {
+    const float disc = sum_z * sum_z - sum_k * (sum_z2 - 1.0f);
+    t_init = gmax + (sum_z - sqrtf(disc)) / sum_k - 1.0f;
+  }
+  t_lo = t_init;
+  t_hi = t_init + 1.0f / kBins;
   t = 0.5f * (t_lo + t_hi);
 }
 
@@ -499,7 +549,10 @@ __device__ __forceinline__ float solve_tau(S& sp, const DecodeArgs& a, const flo
     sp.sync();
     EKV_STAMP(8);
     float t_lo, t_hi;
-    histogram_init(hist, gmax, alpha, t, t_lo, t_hi);
+    if ((alpha == 2.0f || alpha == 1.5f) && n <= kExactInitTokens)
+      histogram_init_wave(hist[kBins - 1 - min(sp.lane, kBins - 1)], gmax, alpha, t, t_lo, t_hi);
+    else
+      histogram_init(hist, gmax, alpha, t, t_lo, t_hi);
     EKV_STAMP(9);
     for (int it = 0; it < a.iters; ++it) {
       float a0, a1, a2;
@@ -560,8 +613,8 @@ struct HeadShared {
   int (*hist)[kBins];
   float4* part;  // [2][kWaves] reduction partials
   float* s_tau;
-  int64_t* sup_row;
-  float* sup_p;  // [G][kHeadThreads]
+  int* sup_row;  // [sup_chunk(G)]
+  float* sup_p;  // [G][sup_chunk(G)]
   int* flag_cnt;
   float* red;    // [kWaves][D]
   int* s_pages;  // [kTablePages]
@@ -642,9 +695,13 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
   __syncthreads();
   EKV_STAMP(3);
 
-  // phase 2: tau per head, one team of waves per head
-  if (n <= kWaveTauMax) {
-    solve_heads<(G >= 4 ? 1 : 4 / G), G>(a, b, h0, n, sc, stride, sh);
+  // phase 2: tau per head, one team of waves per head: 4 / G waves (one per
+  // SIMD) for lists up to 4096 tokens (measured at the headline shape: teams
+  // of 1, 2, 4 and 8 waves took 67.3, 67.0, 66.2 and 66.8 us per step), the
+  // whole workgroup for longer ones
+  constexpr int kTeam = G >= 4 ? 1 : 4 / G;
+  if (n <= 4096) {
+    solve_heads<kTeam, G>(a, b, h0, n, sc, stride, sh);
   } else {
     solve_heads<kWaves / G, G>(a, b, h0, n, sc, stride, sh);
   }
@@ -667,51 +724,65 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
 #pragma unroll
     for (int i = 0; i < VEC; ++i) acc[g][i] = 0.f;
 
-  // The scores (and, from global memory, the page ids) of the next chunk of
-  // tokens are loaded before this chunk's V rows, so they have landed when
-  // the chunk after starts (the loads are clamped to the last token and
-  // issued unconditionally).
-  float s_nx[G];
-  int pg_nx = 0;
+  // The support is compacted a chunk of TPT * kHeadThreads tokens at a time
+  // (TPT tokens per thread; one chunk covers the selections of the common
+  // shapes), and only its V rows are read.  The scores (and, from global
+  // memory, the page ids) of the next chunk are loaded before this chunk's V
+  // rows, so they have landed when the chunk after starts (the loads are
+  // clamped to the last token and issued unconditionally).
+  constexpr int TPT = sup_chunk(G) / kHeadThreads;
+  constexpr int CH = sup_chunk(G);
+  float s_nx[TPT][G];
+  int pg_nx[TPT];
   auto prefetch = [&](int t0) {
-    const int cc = min(t0 + tid, n - 1);
 #pragma unroll
-    for (int g = 0; g < G; ++g) s_nx[g] = sc[g * stride + cc];
-    if (!kTableInLds) pg_nx = pi[cc / ps];
+    for (int j = 0; j < TPT; ++j) {
+      const int cc = min(t0 + j * kHeadThreads + tid, n - 1);
+#pragma unroll
+      for (int g = 0; g < G; ++g) s_nx[j][g] = sc[g * stride + cc];
+      pg_nx[j] = kTableInLds ? 0 : pi[cc / ps];
+    }
   };
   if (n > 0) prefetch(0);
-  for (int t0 = 0; t0 < n; t0 += kHeadThreads) {
-    const int c = t0 + tid;
-    float s_cur[G];
+  for (int t0 = 0; t0 < n; t0 += CH) {
+    float p[TPT][G];
+    bool any[TPT];
+    int row[TPT];
+    uint64_t m[TPT];
+    int mine = 0;
 #pragma unroll
-    for (int g = 0; g < G; ++g) s_cur[g] = s_nx[g];
-    const int pg = pg_nx;
-    if (t0 + kHeadThreads < n) prefetch(t0 + kHeadThreads);
-    float p[G];
-    bool any = false;
-    int64_t row = -1;
-    if (c < n) {
+    for (int j = 0; j < TPT; ++j) {
+      const int c = t0 + j * kHeadThreads + tid;
+      any[j] = false;
+      row[j] = -1;
+      if (c < n) {
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float s = s_cur[g];
-        p[g] = 0.f;
-        if (s > tau[g]) {
-          p[g] = entmax_weight(s - tau[g], alpha, c0);
-          any = true;
+        for (int g = 0; g < G; ++g) {
+          const float sv = s_nx[j][g];
+          p[j][g] = 0.f;
+          if (sv > tau[g]) {
+            p[j][g] = entmax_weight(sv - tau[g], alpha, c0);
+            any[j] = true;
+          }
+        }
+        if (any[j]) {
+          int64_t r;
+          if (kTableInLds) {
+            r = token_row(sh.s_pages, c, ps, a.row_limit);
+          } else {
+            const int pg = pg_nx[j];
+            r = (int64_t)pg * ps + (c % ps);
+            r = (pg >= 0 && r < a.row_limit) ? r : -1;
+          }
+          row[j] = (int)r;
+          if (r < 0) any[j] = false;
         }
       }
-      if (any) {
-        if (kTableInLds) {
-          row = token_row(sh.s_pages, c, ps, a.row_limit);
-        } else {
-          const int64_t r = (int64_t)pg * ps + (c % ps);
-          row = (pg >= 0 && r < a.row_limit) ? r : -1;
-        }
-        if (row < 0) any = false;
-      }
+      m[j] = __ballot(any[j]);
+      mine += __popcll(m[j]);
     }
-    const uint64_t m = __ballot(any);
-    if (lane == 0) sh.flag_cnt[wid] = __popcll(m);
+    if (t0 + CH < n) prefetch(t0 + CH);
+    if (lane == 0) sh.flag_cnt[wid] = mine;
     __syncthreads();
     int before = 0, nsup = 0;
 #pragma unroll
@@ -720,12 +791,16 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
       before += (w < wid) ? cw : 0;
       nsup += cw;
     }
-    if (any) {
-      const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-      const int slot = before + __popcll(m & below);
-      sh.sup_row[slot] = row;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
-      for (int g = 0; g < G; ++g) sh.sup_p[g * kHeadThreads + slot] = p[g];
+    for (int j = 0; j < TPT; ++j) {
+      if (any[j]) {
+        const int slot = before + __popcll(m[j] & below);
+        sh.sup_row[slot] = row[j];
+#pragma unroll
+        for (int g = 0; g < G; ++g) sh.sup_p[g * CH + slot] = p[j][g];
+      }
+      before += __popcll(m[j]);
     }
     __syncthreads();
     // eight support rows per segment in flight, kept raw until converted (a
@@ -734,7 +809,8 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
     for (int j0 = seg; j0 < nsup; j0 += R * SEGS) {
       uint4 x[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) x[r] = ld16(vh + sh.sup_row[min(j0 + r * SEGS, nsup - 1)] * a.ksr + col);
+      for (int r = 0; r < R; ++r)
+        x[r] = ld16(vh + (int64_t)sh.sup_row[min(j0 + r * SEGS, nsup - 1)] * a.ksr + col);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int j = j0 + r * SEGS;
@@ -742,7 +818,7 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
           const T* e = reinterpret_cast<const T*>(&x[r]);
 #pragma unroll
           for (int g = 0; g < G; ++g) {
-            const float w = sh.sup_p[g * kHeadThreads + j];
+            const float w = sh.sup_p[g * CH + j];
 #pragma unroll
             for (int i = 0; i < VEC; ++i) acc[g][i] += w * to_f<T>(e[i]);
           }
@@ -784,8 +860,8 @@ __global__ __launch_bounds__(kHeadThreads) void decode_head_kernel(DecodeArgs a)
   __shared__ __attribute__((aligned(16))) int hist[kWaves][kBins];
   __shared__ float4 part[2 * kWaves];
   __shared__ float s_tau[G];
-  __shared__ int64_t sup_row[kHeadThreads];
-  __shared__ float sup_p[G * kHeadThreads];
+  __shared__ int sup_row[sup_chunk(G)];
+  __shared__ float sup_p[G * sup_chunk(G)];
   __shared__ int flag_cnt[kWaves];
   __shared__ float red[kWaves * D];
   __shared__ int s_pages[kTablePages];
@@ -834,18 +910,25 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
   __shared__ __attribute__((aligned(16))) int hist[kWaves][kBins];
   __shared__ float4 part[2 * kWaves];
   __shared__ float s_tau[G];
-  __shared__ int64_t sup_row[kHeadThreads];
-  __shared__ float sup_p[G * kHeadThreads];
+  __shared__ int sup_row[sup_chunk(G)];
+  __shared__ float sup_p[G * sup_chunk(G)];
   __shared__ int flag_cnt[kWaves];
   __shared__ float red[kWaves * D];
   __shared__ int s_pages[kTablePages];
   __shared__ float wmax[G * kWaves];
+  // G == 1: the select's radix histograms; the scan fills the first
+  __shared__ unsigned sel_hist[G == 1 ? topk::ScoreKey<T>::kBits / 8 : 1][256];
   HeadShared sh{hist, part, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
   sh.wmax = wmax;
 
   const int bkv = blockIdx.x;
   const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
   uint32_t* keys = reinterpret_cast<uint32_t*>(stage);
+  if (G == 1) {
+    for (int i = threadIdx.x; i < (int)(sizeof(sel_hist) / 4); i += kHeadThreads)
+      (&sel_hist[0][0])[i] = 0u;
+    __syncthreads();
+  }
   const topk::Ragged r = topk::ragged_topk(t.seq_lens, b, a.page_size, t.num_pages, t.seq_len,
                                            t.q_pos, t.k, t.last_page);
   const bool keep = r.count <= t.key_cap;
@@ -858,7 +941,8 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
     topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC>(
         (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
         a.slopes, (T*)t.scores, a.H, t.num_pages, r.count, a.page_size, r.seq_len, r.q_pos, b,
-        kvh, G == 1 ? (keep ? keys : nullptr) : head_keys);
+        kvh, G == 1 ? (keep ? keys : nullptr) : head_keys,
+        G == 1 && keep ? &sel_hist[0][0] : nullptr);
   } else if (G > 1 && head_keys) {
     // every query head's keys into LDS once (the select reads them per pass)
     for (int i = threadIdx.x; i < G * r.count; i += kHeadThreads) {
@@ -871,13 +955,18 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
   int32_t* pi = const_cast<int32_t*>(a.page_indices) + b * a.pisb + kvh * a.pish;
   // G == 1: the scan left the keys in LDS; prescored, the select stages them
   const bool staged = keep && !t.prescored;
-  topk::topk_select_block<T, G, kHeadThreads>(sbase, t.num_pages, r.count, r.k, r.last_page, pi,
-                                              keys, keep ? r.count : 0, staged, s_pages, list,
-                                              head_keys, t.num_pages, t.list_words);
+  // the page table goes to LDS only here and to global memory at the end, so
+  // that no barrier of the select or the decode waits on its stores
+  topk::topk_select_block<T, G, kHeadThreads>(
+      sbase, t.num_pages, r.count, r.k, r.last_page, nullptr, keys, keep ? r.count : 0, staged,
+      s_pages, list, head_keys, t.num_pages, t.list_words, G == 1 ? sel_hist : nullptr,
+      G == 1 && staged);
   __syncthreads();
   EKV_STAMP(2);
   const int n = token_count(a, b, kvh);
   decode_head_body<T, LPR, G, UD, true, true>(a, b, kvh, n, stage, a.stage_cap, sh);
+  const int slots = min(r.k, r.count) + (r.last_page >= 0 ? 1 : 0);
+  for (int i = threadIdx.x; i < slots; i += kHeadThreads) pi[i] = s_pages[i];
 }
 
 // Gaussian selection of one step, as read by the fused kernel (see
@@ -911,8 +1000,8 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
   __shared__ __attribute__((aligned(16))) int hist[kWaves][kBins];
   __shared__ float4 part[2 * kWaves];
   __shared__ float s_tau[G];
-  __shared__ int64_t sup_row[kHeadThreads];
-  __shared__ float sup_p[G * kHeadThreads];
+  __shared__ int sup_row[sup_chunk(G)];
+  __shared__ float sup_p[G * sup_chunk(G)];
   __shared__ int flag_cnt[kWaves];
   __shared__ float red[kWaves * D];
   __shared__ int s_pages[kTablePages];

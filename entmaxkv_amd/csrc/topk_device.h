@@ -119,7 +119,7 @@ __device__ __forceinline__ void wave_hist_add(unsigned* hist, uint32_t bin, bool
 template <int NT, int kBits, typename KeyOf, bool kAggregate = false>
 __device__ __forceinline__ void radix_threshold(KeyOf key_of, int n, int k,
                                                 unsigned (*hist)[256], uint32_t& thr,
-                                                int& kk) {
+                                                int& kk, const unsigned* pass0 = nullptr) {
   constexpr int kPasses = kBits / 8;
   constexpr int kBatch = 8;
   const int tid = threadIdx.x;
@@ -129,32 +129,39 @@ __device__ __forceinline__ void radix_threshold(KeyOf key_of, int n, int k,
 #pragma unroll
   for (int pass = 0; pass < kPasses; ++pass) {
     const int shift = kBits - 8 * (pass + 1);
-    for (int p0 = 0; p0 < n; p0 += NT * kBatch) {
-      uint32_t kv[kBatch];
+    // pass 0 may come prebuilt (the criticality scan adds every key's top
+    // digit as it goes) and already visible to every thread
+    const bool prebuilt = pass == 0 && pass0 != nullptr;
+    const unsigned* hp = prebuilt ? pass0 : hist[pass];
+    if (!prebuilt) {
+      for (int p0 = 0; p0 < n; p0 += NT * kBatch) {
+        uint32_t kv[kBatch];
 #pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int p = p0 + j * NT + tid;
-        kv[j] = p < n ? key_of(p) : 0u;
-      }
+        for (int j = 0; j < kBatch; ++j) {
+          const int p = p0 + j * NT + tid;
+          kv[j] = p < n ? key_of(p) : 0u;
+        }
 #pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const int p = p0 + j * NT + tid;
-        const bool act = p < n && (kv[j] & pmask) == prefix;
-        const uint32_t bin = (kv[j] >> shift) & 255u;
-        if (pass == 0 || kAggregate) {
-          // wave-uniform: every lane takes part in the ballots
-          if (p0 + j * NT < n) wave_hist_add(hist[pass], bin, act);
-        } else if (act) {
-          atomicAdd(&hist[pass][bin], 1u);
+        for (int j = 0; j < kBatch; ++j) {
+          const int p = p0 + j * NT + tid;
+          const bool act = p < n && (kv[j] & pmask) == prefix;
+          const uint32_t bin = (kv[j] >> shift) & 255u;
+          if (pass == 0 || kAggregate) {
+            // wave-uniform: every lane takes part in the ballots
+            if (p0 + j * NT < n) wave_hist_add(hist[pass], bin, act);
+          } else if (act) {
+            atomicAdd(&hist[pass][bin], 1u);
+          }
         }
       }
+      __syncthreads();
     }
-    __syncthreads();
+    EKV_CSTAMP(12 + pass);
     // lane l holds bins 255-4l .. 252-4l; the bin where the count from the
     // top reaches kk is found by every wave independently
     const int top = 255 - 4 * lane;
-    const int c0 = (int)hist[pass][top], c1 = (int)hist[pass][top - 1];
-    const int c2 = (int)hist[pass][top - 2], c3 = (int)hist[pass][top - 3];
+    const int c0 = (int)hp[top], c1 = (int)hp[top - 1];
+    const int c2 = (int)hp[top - 2], c3 = (int)hp[top - 3];
     const int sum = c0 + c1 + c2 + c3;
     const int incl = wave_incl_scan(sum);
     const int excl = incl - sum;
@@ -223,6 +230,7 @@ __device__ __forceinline__ void pack_selected(KeyOf key_of, int n, bool take_all
     wave_cnt[2 * wid + 1] = eq_n;
   }
   __syncthreads();
+  EKV_CSTAMP(14);
   int gt_base = 0, eq_base = 0;
   for (int w = 0; w < wid; ++w) {
     gt_base += wave_cnt[2 * w];
@@ -394,11 +402,17 @@ __host__ __device__ constexpr int group_list_words(int G, int k, bool concurrent
 // ascending page ids to out[0..k) (and lds_out[0..k) when non-null) and
 // `last_page` to out[k] when last_page >= 0.  blockDim == NT.
 //
+// `out` may be null: the table then goes to lds_out only (the caller stores
+// it later, so that no barrier waits on the global stores).
+//
 // G == 1: the head's own order keys.  They come from `lds_keys` when
 // `prestaged`, are staged there first when they fit (`lds_cap` keys), and are
 // otherwise recomputed from the scores on every pass (the scores must be
 // visible to this workgroup: written by a previous launch or by this
-// workgroup).
+// workgroup).  `ext_hist` (kBits / 8 histograms of 256 bins, zero and visible
+// on entry) replaces the select's own histograms; with `pass0_built` its
+// first histogram already counts every key's top 8 bits (the criticality
+// scan built it), which saves a pass and a barrier.
 //
 // G > 1 (the group shares one page table; no reference counterpart): pages
 // are taken by their best rank over the group's query heads, ties to the lower
@@ -420,7 +434,9 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
                                                   int* lds_out = nullptr,
                                                   uint32_t* lds_list = nullptr,
                                                   const uint32_t* head_keys = nullptr,
-                                                  int hk_stride = 0, int list_words = 0) {
+                                                  int hk_stride = 0, int list_words = 0,
+                                                  unsigned (*ext_hist)[256] = nullptr,
+                                                  bool pass0_built = false) {
   constexpr int W = NT / 64;
   constexpr int kBits = ScoreKey<T>::kBits;
   constexpr int kPasses = kBits / 8;
@@ -431,7 +447,7 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
   k = min(k, num_pages);
   const bool take_all = (k == num_pages);
   auto emit_out = [&](int slot, int p, uint32_t) {
-    out[slot] = p;
+    if (out) out[slot] = p;
     if (lds_out) lds_out[slot] = p;
   };
   auto zero_hist = [&]() {
@@ -441,7 +457,8 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
     const bool staged = prestaged || num_pages <= lds_cap;
     auto own = [&](int p) -> uint32_t { return ScoreKey<T>::key(s0[p]); };
     auto key_of = [&](int p) -> uint32_t { return staged ? lds_keys[p] : own(p); };
-    zero_hist();
+    unsigned (*hs)[256] = ext_hist ? ext_hist : hist;
+    if (!ext_hist) zero_hist();
     if (staged && !prestaged) {
       for (int p0 = 0; p0 < num_pages; p0 += NT * kBatch) {
         uint32_t kv[kBatch];
@@ -457,11 +474,13 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
         }
       }
     }
-    __syncthreads();
+    if (!ext_hist || (staged && !prestaged)) __syncthreads();
     EKV_CSTAMP(2);
     uint32_t thr = 0;
     int kk = 0;
-    if (k > 0 && !take_all) radix_threshold<NT, kBits>(key_of, num_pages, k, hist, thr, kk);
+    if (k > 0 && !take_all)
+      radix_threshold<NT, kBits>(key_of, num_pages, k, hs, thr, kk,
+                                 ext_hist && pass0_built ? ext_hist[0] : nullptr);
     EKV_CSTAMP(3);
     if (k > 0) pack_selected<NT>(key_of, num_pages, take_all, thr, kk, wave_cnt, emit_out);
   } else {
@@ -583,7 +602,7 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
     }
   }
   if (tid == 0 && last_page >= 0) {
-    out[k] = last_page;
+    if (out) out[k] = last_page;
     if (lds_out) lds_out[k] = last_page;
   }
   EKV_CSTAMP(4);
@@ -593,15 +612,18 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
 // of the G query heads for pages [0, count) written to `scores`
 // ([B, H, stride], query dtype; count <= stride) and, when `lds_keys` is
 // non-null, the order keys kept there: lds_keys[p] for G == 1, lds_keys[g *
-// stride + p] per query head for G > 1.  A row segment of LPR lanes
-// owns one page and loads its min and max rows with 16-byte loads, U pages
-// per segment in flight.  Returns the head's score base pointer.
+// stride + p] per query head for G > 1; for G == 1 with `hist0` (256 bins,
+// zero and visible on entry) every key's top 8 bits are counted there too.  A
+// row segment of LPR lanes owns one page and loads its min and max rows with
+// 16-byte loads, U pages per segment in flight.  Returns the head's score
+// base pointer.
 template <typename T, int LPR, int G, int NT, int U>
 __device__ __forceinline__ T* criticality_scan_head(
     const T* __restrict__ q, int64_t qsb, int64_t qsh, const T* __restrict__ kmin,
     const T* __restrict__ kmax, int64_t ssb, int64_t ssh, int64_t ssp,
     const float* __restrict__ slopes, T* __restrict__ scores, int H, int stride, int num_pages,
-    int page_size, int seq_len, int q_pos, int b, int kvh, uint32_t* lds_keys) {
+    int page_size, int seq_len, int q_pos, int b, int kvh, uint32_t* lds_keys,
+    unsigned* hist0 = nullptr) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int SEGS = NT / LPR;
   constexpr int ROUND = SEGS * U;
@@ -654,7 +676,10 @@ __device__ __forceinline__ T* criticality_scan_head(
           if (G > 1 && keep_keys) lds_keys[g * stride + p] = key;
         }
       }
-      if (G == 1 && keep_keys && p < num_pages && sl == 0) lds_keys[p] = key;
+      if (G == 1 && keep_keys && p < num_pages && sl == 0) {
+        lds_keys[p] = key;
+        if (hist0) atomicAdd(&hist0[key >> (ScoreKey<T>::kBits - 8)], 1u);
+      }
     }
   }
   return sbase;
