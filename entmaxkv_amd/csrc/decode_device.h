@@ -28,6 +28,11 @@
 // per-workgroup wall-clock stamps (100 MHz) of the fused kernels' phases.
 #ifdef EKV_PHASE_TIMERS
 __device__ unsigned long long ekv_phase_timers[4096 * 16];
+// per-wave stamps: [block < 256][wave][slot < 8]
+__device__ unsigned long long ekv_wave_timers[256 * 16 * 8];
+#define EKV_WSTAMP(i)                                                    \
+  if ((threadIdx.x & 63) == 0 && blockIdx.x < 256)                       \
+  ekv_wave_timers[(blockIdx.x * 16 + (threadIdx.x >> 6)) * 8 + (i)] = wall_clock64()
 #define EKV_STAMP(i) \
   if (threadIdx.x == 0 && blockIdx.x < 4096) ekv_phase_timers[blockIdx.x * 16 + (i)] = wall_clock64()
 // slot 6 in the top-k launch: the top-k threshold found (topk_device.h stamp
@@ -42,6 +47,7 @@ __device__ unsigned long long ekv_phase_timers[4096 * 16];
   } while (0)
 #else
 #define EKV_STAMP(i)
+#define EKV_WSTAMP(i)
 #endif
 
 #include "ekv_common.h"
@@ -138,6 +144,161 @@ __device__ __forceinline__ void load_query(const DecodeArgs& a, int b, int h0, i
   }
 }
 
+// ---------------------------------------------------------------------------
+// GQA scoring on the matrix cores
+// ---------------------------------------------------------------------------
+//
+// With G query heads per kv head the scores of 16 tokens are a 16 x D by
+// D x G product.  v_mfma_f32_16x16x32_{f16,bf16} computes a 16 x 16 tile of
+// it per 32-wide slice of D (G of the 16 columns used), in place of G dot
+// products and G 16-lane reductions per token on the VALU, which bound the
+// scoring phase for G >= 2.  Operand layout (lane l, measured on gfx950):
+// A[l % 16][8 (l / 16) + e] (e < 8), B[8 (l / 16) + e][l % 16], and the
+// result C[4 (l / 16) + r][l % 16] (r < 4).  Products of 16-bit values are
+// exact in fp32 and the accumulation is fp32, as on the VALU path; only the
+// summation order differs.
+#ifndef EKV_MFMA_MIN_G
+#define EKV_MFMA_MIN_G 2
+#endif
+template <typename T> struct Mfma16;
+typedef _Float16 ekv_f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 ekv_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float ekv_f32x4 __attribute__((ext_vector_type(4)));
+template <> struct Mfma16<_Float16> {
+  static __device__ __forceinline__ ekv_f32x4 mac(const uint4& a, const uint4& b, ekv_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(ekv_f16x8, a),
+                                                  __builtin_bit_cast(ekv_f16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<bf16_t> {
+  static __device__ __forceinline__ ekv_f32x4 mac(const uint4& a, const uint4& b, ekv_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(ekv_bf16x8, a),
+                                                   __builtin_bit_cast(ekv_bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <typename T, int G>
+constexpr bool kScoreMfma = (sizeof(T) == 2) && G >= EKV_MFMA_MIN_G;
+
+// score_rows on the matrix cores (see kScoreMfma): every wave scores tiles of
+// 16 consecutive compacted tokens, U tiles per round, two rounds in flight.
+template <typename T, int LPR, int G, int NT, int U, typename PagePtr>
+__device__ __forceinline__ void score_rows_mfma(const DecodeArgs& a, int b, int kvh, int c_begin,
+                                                int c_end, float* sc, int64_t stride,
+                                                PagePtr pages, int c_base, float* run_max) {
+  constexpr int D = LPR * 8;
+  constexpr int KB = D / 32;  // 32-wide slices of D
+  constexpr int W = NT / 64;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int j = lane & 15;   // A row within the tile; B / C column (query head)
+  const int kq = lane >> 4;  // 8-element block within each slice
+  const int h0 = kvh * G;
+  // B: head j's query (scaled by qscale, rounded to T) at k = 32 i + 8 kq .. +7
+  uint4 qb[KB];
+  {
+    const T* qh = (const T*)a.q + b * a.qsb + (h0 + min(j, G - 1)) * a.qsh;
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      Vec<T> x;
+      x.load(qh + 32 * i + 8 * kq);
+      T tmp[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tmp[e] = from_f<T>(j < G ? x.v[e] * a.qscale : 0.f);
+      qb[i] = *reinterpret_cast<const uint4*>(tmp);
+    }
+  }
+  float slope = 0.f;
+  int q_idx = 0;
+  if (a.slopes) {
+    q_idx = (a.q_seqlens ? a.q_seqlens[b] : a.cache_seqlens[b * a.csb + kvh * a.csh]) - 1;
+    slope = j < G ? a.slopes[h0 + j] * (a.alpha - 1.0f) : 0.f;
+  }
+  const T* kh = (const T*)a.k + b * a.ksb + kvh * a.ksh;
+  const bool kpos = a.slopes && a.positions;
+  const int ps = a.page_size;
+  constexpr int kNoRow = INT_MIN;
+  auto row_of = [&](int c) -> int {
+    const int page = pages[(c - c_base) / ps];
+    const int64_t row = (int64_t)page * ps + (c % ps);
+    return (page >= 0 && row < a.row_limit) ? (int)row : kNoRow;
+  };
+  float rmax = -1.0e6f;
+  // tile t covers tokens c_begin + 16 t .. + 15; wave wid takes tiles wid + W (u + U m)
+  auto fetch = [&](int m, uint4 (&kv)[U][KB]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c_begin + ((m * U + u) * W + wid) * 16 + j;
+      const int row = c < c_end ? row_of(c) : kNoRow;
+      const T* kr = kh + (int64_t)max(row, 0) * a.ksr + 8 * kq;
+#pragma unroll
+      for (int i = 0; i < KB; ++i) kv[u][i] = ld16(kr + 32 * i);
+    }
+  };
+  auto consume = [&](int m, const uint4 (&kv)[U][KB]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      ekv_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < KB; ++i) acc = Mfma16<T>::mac(kv[u][i], qb[i], acc);
+      const int t0 = c_begin + ((m * U + u) * W + wid) * 16 + 4 * kq;
+      if (j < G) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int c = t0 + r;
+          if (c < c_end) {
+            const int row = row_of(c);
+            float s = acc[r];
+            if (row == kNoRow) s = -INFINITY;
+            else if (a.slopes && !kpos) s += slope * (float)(row - q_idx);
+            sc[j * stride + c] = s;
+            if (!kpos) rmax = fmaxf(rmax, s);
+          }
+        }
+      }
+    }
+  };
+  const int tiles = c_end > c_begin ? (c_end - c_begin + 15) / 16 : 0;
+  const int rounds = (tiles + U * W - 1) / (U * W);
+  uint4 kv_a[U][KB], kv_b[U][KB];
+  if (rounds > 0) fetch(0, kv_a);
+  int r = 0;
+  for (; r + 2 < rounds; r += 2) {
+    fetch(r + 1, kv_b);
+    consume(r, kv_a);
+    fetch(r + 2, kv_a);
+    consume(r + 1, kv_b);
+  }
+  if (r + 1 < rounds) {
+    fetch(r + 1, kv_b);
+    consume(r, kv_a);
+    consume(r + 1, kv_b);
+  } else if (r < rounds) {
+    consume(r, kv_a);
+  }
+  if (kpos && j < G) {
+    // explicit key positions: the ALiBi term over the scores this lane wrote
+    // above (out of the scoring loop, as in score_rows)
+    const int32_t* pos = a.positions + b * a.posb + kvh * a.posh;
+    for (int m = 0; m < rounds; ++m) {
+      for (int u = 0; u < U; ++u) {
+        const int t0 = c_begin + ((m * U + u) * W + wid) * 16 + 4 * kq;
+        for (int rr = 0; rr < 4; ++rr) {
+          const int c = t0 + rr;
+          if (c >= c_end) continue;
+          const int row = row_of(c);
+          float s = sc[j * stride + c];
+          if (row != kNoRow) s += slope * (float)(pos[row] - q_idx);
+          sc[j * stride + c] = s;
+          rmax = fmaxf(rmax, s);
+        }
+      }
+    }
+  }
+  if (run_max) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) run_max[g] = fmaxf(run_max[g], j == g ? rmax : -1.0e6f);
+  }
+}
+
 // Scores of compacted tokens [c_begin, c_end) of one (b, kv head) for its G
 // heads: sc[g * stride + c].  NT threads, rows of LPR lanes, U rows per
 // segment in flight.  `pages` holds the page ids of tokens from `c_base` on
@@ -153,6 +314,10 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
   const int sl = threadIdx.x % LPR;
   const int col = sl * VEC;
   const int h0 = kvh * G;
+  if constexpr (kScoreMfma<T, G>) {
+    score_rows_mfma<T, LPR, G, NT, 2>(a, b, kvh, c_begin, c_end, sc, stride, pages, c_base,
+                                      run_max);
+  } else {
   uint4 qraw[G];
   load_query<T, G>(a, b, h0, col, qraw);
   float slope[G];
@@ -202,16 +367,27 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
     }
   };
   // two register buffers: the loads of the next round are issued before the
-  // current round's arithmetic
+  // current round's arithmetic.  The steady-state loop issues both rounds'
+  // loads unconditionally, so the compiler's wait counts keep the other
+  // buffer's loads in flight during each consume; the last one or two rounds
+  // are peeled.
   int rows_a[U], rows_b[U];
   uint4 kv_a[U], kv_b[U];
-  if (c_begin < c_end) fetch(c_begin, rows_a, kv_a);
-  for (int c0 = c_begin; c0 < c_end; c0 += 2 * ROWS) {
-    if (c0 + ROWS < c_end) fetch(c0 + ROWS, rows_b, kv_b);
-    consume(c0, rows_a, kv_a);
-    if (c0 + ROWS >= c_end) break;
-    if (c0 + 2 * ROWS < c_end) fetch(c0 + 2 * ROWS, rows_a, kv_a);
-    consume(c0 + ROWS, rows_b, kv_b);
+  const int rounds = c_end > c_begin ? (c_end - c_begin + ROWS - 1) / ROWS : 0;
+  if (rounds > 0) fetch(c_begin, rows_a, kv_a);
+  int r = 0;
+  for (; r + 2 < rounds; r += 2) {
+    fetch(c_begin + (r + 1) * ROWS, rows_b, kv_b);
+    consume(c_begin + r * ROWS, rows_a, kv_a);
+    fetch(c_begin + (r + 2) * ROWS, rows_a, kv_a);
+    consume(c_begin + (r + 1) * ROWS, rows_b, kv_b);
+  }
+  if (r + 1 < rounds) {
+    fetch(c_begin + (r + 1) * ROWS, rows_b, kv_b);
+    consume(c_begin + r * ROWS, rows_a, kv_a);
+    consume(c_begin + (r + 1) * ROWS, rows_b, kv_b);
+  } else if (r < rounds) {
+    consume(c_begin + r * ROWS, rows_a, kv_a);
   }
   if (kpos && sl == 0) {
     // explicit key positions: the ALiBi term (and the running max) over the
@@ -232,6 +408,7 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
         if (run_max) run_max[g] = fmaxf(run_max[g], s);
       }
     }
+  }
   }
 }
 
@@ -692,14 +869,16 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
       if (lane == 0) sh.wmax[g * kWaves + wid] = m;
     }
   }
+  EKV_WSTAMP(5);
   __syncthreads();
   EKV_STAMP(3);
 
-  // phase 2: tau per head, one team of waves per head: 4 / G waves (one per
-  // SIMD) for lists up to 4096 tokens (measured at the headline shape: teams
-  // of 1, 2, 4 and 8 waves took 67.3, 67.0, 66.2 and 66.8 us per step), the
-  // whole workgroup for longer ones
-  constexpr int kTeam = G >= 4 ? 1 : 4 / G;
+  // phase 2: tau per head, one team of waves per head: for lists up to 4096
+  // tokens 4 / G waves (one per SIMD; G = 1 at the headline shape: teams of 1,
+  // 2, 4 and 8 waves took 67.3, 67.0, 66.2 and 66.8 us per step), or kWaves /
+  // G for G >= 4 (config 4: 4 waves per head 133.2 us against one wave 135.1
+  // us); the whole workgroup for longer lists
+  constexpr int kTeam = G >= 4 ? kWaves / G : 4 / G;
   if (n <= 4096) {
     solve_heads<kTeam, G>(a, b, h0, n, sc, stride, sh);
   } else {
@@ -944,10 +1123,21 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
         kvh, G == 1 ? (keep ? keys : nullptr) : head_keys,
         G == 1 && keep ? &sel_hist[0][0] : nullptr);
   } else if (G > 1 && head_keys) {
-    // every query head's keys into LDS once (the select reads them per pass)
-    for (int i = threadIdx.x; i < G * r.count; i += kHeadThreads) {
-      const int g = i / r.count, p = i % r.count;
-      head_keys[g * t.num_pages + p] = topk::ScoreKey<T>::key(sbase[g * t.num_pages + p]);
+    // every query head's keys into LDS once (the select reads them per pass);
+    // eight loads per thread in flight before their stores
+    const int total = G * r.count;
+    for (int i0 = 0; i0 < total; i0 += 8 * kHeadThreads) {
+      T sv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = min(i0 + j * kHeadThreads + (int)threadIdx.x, total - 1);
+        sv[j] = sbase[(i / r.count) * t.num_pages + i % r.count];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = i0 + j * kHeadThreads + (int)threadIdx.x;
+        if (i < total) head_keys[(i / r.count) * t.num_pages + i % r.count] = topk::ScoreKey<T>::key(sv[j]);
+      }
     }
   }
   __syncthreads();
@@ -961,6 +1151,7 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
       sbase, t.num_pages, r.count, r.k, r.last_page, nullptr, keys, keep ? r.count : 0, staged,
       s_pages, list, head_keys, t.num_pages, t.list_words, G == 1 ? sel_hist : nullptr,
       G == 1 && staged);
+  EKV_WSTAMP(4);
   __syncthreads();
   EKV_STAMP(2);
   const int n = token_count(a, b, kvh);

@@ -16,6 +16,10 @@ template struct ekv::dec::Launch<ekv::bf16_t, EKV_INST_G>;
 #endif
 
 #ifdef EKV_PHASE_TIMERS
+extern "C" int ekv_debug_wave_timers(unsigned long long* host, int n) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(ekv_wave_timers),
+                                  n * sizeof(unsigned long long));
+}
 extern "C" int ekv_debug_phase_timers(unsigned long long* host, int n) {
   return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(ekv_phase_timers),
                                   n * sizeof(unsigned long long));

@@ -9,6 +9,9 @@
 #ifndef EKV_CSTAMP
 #define EKV_CSTAMP(i)
 #endif
+#ifndef EKV_WSTAMP
+#define EKV_WSTAMP(i)
+#endif
 
 namespace ekv {
 namespace topk {
@@ -154,6 +157,7 @@ __device__ __forceinline__ void radix_threshold(KeyOf key_of, int n, int k,
           }
         }
       }
+      EKV_WSTAMP(1 + pass);
       __syncthreads();
     }
     EKV_CSTAMP(12 + pass);
@@ -229,6 +233,7 @@ __device__ __forceinline__ void pack_selected(KeyOf key_of, int n, bool take_all
     wave_cnt[2 * wid] = gt_n;
     wave_cnt[2 * wid + 1] = eq_n;
   }
+  EKV_WSTAMP(3);
   __syncthreads();
   EKV_CSTAMP(14);
   int gt_base = 0, eq_base = 0;
@@ -682,6 +687,7 @@ __device__ __forceinline__ T* criticality_scan_head(
       }
     }
   }
+  EKV_WSTAMP(0);
   return sbase;
 }
 
