@@ -160,7 +160,6 @@ __device__ __forceinline__ void radix_threshold(KeyOf key_of, int n, int k,
       EKV_WSTAMP(1 + pass);
       __syncthreads();
     }
-    EKV_CSTAMP(12 + pass);
     // lane l holds bins 255-4l .. 252-4l; the bin where the count from the
     // top reaches kk is found by every wave independently
     const int top = 255 - 4 * lane;
@@ -397,6 +396,146 @@ __device__ __forceinline__ void pack_selected_group(KeyOf key_of, int n,
   }
 }
 
+// Pages the sorted group select handles (a multiple of its workgroup size).
+constexpr int kGroupSortedPages = 4096;
+
+template <int G>
+__device__ __forceinline__ int total_of(const int (&t)[G], int g) {
+  int r = 0;
+#pragma unroll
+  for (int i = 0; i < G; ++i) r = i == g ? t[i] : r;
+  return r;
+}
+
+__host__ __device__ constexpr int next_pow2_int(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+// The group top-k of topk_select_block for 16-bit keys, given each head's
+// radix threshold thr[g] (its k-th largest key): every head's keys >= thr[g]
+// go to its segment of `cand` (C2 words, G * C2 <= NT; `cnt` holds G * NT / 64
+// ints) as
+// (key << 16) | (0xffff - page); a candidate's rank is the number of its
+// head's candidates with a larger composite (key descending, ties to the
+// lower page), so ranks below k are the head's top-k; `level` (num_pages
+// words) takes each page's best (rank * G + head) by atomicMin, `lvl` (k words) counts the pages whose best
+// rank is r, and the smallest r* with at least k pages of rank <= r* gives
+// the final selection: every page of level < r* and the lowest-numbered
+// pages of level r*, packed in ascending page order by pack_selected.
+template <int NT, int G, typename KeyGP, typename Emit>
+__device__ __forceinline__ void group_select_sorted(KeyGP key_gp, int num_pages, int k,
+                                                    const uint32_t (&thr)[G], int C2,
+                                                    uint32_t* cand, uint32_t* level,
+                                                    unsigned* lvl, int* cnt, int* wave_cnt,
+                                                    Emit emit) {
+  constexpr int W = NT / 64;
+  constexpr int IT = kGroupSortedPages / NT;  // pages per thread
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  // candidate flags of this thread's pages (page p0 * NT + tid), all keys
+  // read before any use; per-wave counts, then one barrier for the offsets
+  uint32_t key[IT][G];
+  uint64_t m[IT][G];
+  int wc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) wc[g] = 0;
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int p = it * NT + tid;
+#pragma unroll
+    for (int g = 0; g < G; ++g) key[it][g] = p < num_pages ? key_gp(g, p) : 0u;
+  }
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int p = it * NT + tid;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[it][g] = __ballot(p < num_pages && key[it][g] >= thr[g]);
+      wc[g] += __popcll(m[it][g]);
+    }
+  }
+  __syncthreads();  // the threshold histograms (lvl aliases them) are read
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) cnt[g * W + wid] = wc[g];
+  }
+  for (int p = tid; p < num_pages; p += NT) level[p] = 0xffffffffu;
+  for (int i = tid; i < k; i += NT) lvl[i] = 0u;
+  __syncthreads();
+  int total[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    int base = 0, tot = 0;
+    for (int w = 0; w < W; ++w) {
+      const int c = cnt[g * W + w];
+      base += w < wid ? c : 0;
+      tot += c;
+    }
+    total[g] = tot;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int p = it * NT + tid;
+      if ((m[it][g] >> lane) & 1ull)
+        cand[g * C2 + base + __popcll(m[it][g] & below)] = (key[it][g] << 16) | (0xffffu - (uint32_t)p);
+      base += __popcll(m[it][g]);
+    }
+    // zero padding up to a multiple of 4 for the four-wide reads below
+    if (tid < 3 && tot + tid < C2) cand[g * C2 + tot + tid] = 0u;
+  }
+  __syncthreads();
+  EKV_CSTAMP(13);
+  // rank of a candidate within its head: how many of the head's candidates
+  // order before it (larger composite; the padding never does); one
+  // candidate per thread (G * C2 <= NT), eight four-wide LDS reads in flight
+  const int e = tid;
+  const int g = e / C2, slot = e % C2;
+  uint32_t c = 0, rank = 0;
+  if (e < G * C2 && slot < total_of(total, g)) {
+    const uint32_t* seg = cand + g * C2;
+    c = seg[slot];
+    const uint4* s4 = reinterpret_cast<const uint4*>(seg);
+    const int n4 = (total_of(total, g) + 3) / 4;
+#pragma unroll 8
+    for (int j = 0; j < n4; ++j) {
+      const uint4 x = s4[j];
+      rank += (x.x > c) + (x.y > c) + (x.z > c) + (x.w > c);
+    }
+    if ((int)rank < k) atomicMin(&level[0xffffu - (c & 0xffffu)], rank * (uint32_t)G + (uint32_t)g);
+  }
+  __syncthreads();
+  EKV_CSTAMP(15);
+  // each page counted once, by its best (rank, head) entry
+  if (c != 0u && (int)rank < k &&
+      level[0xffffu - (c & 0xffffu)] == rank * (uint32_t)G + (uint32_t)g)
+    atomicAdd(&lvl[rank], 1u);
+  __syncthreads();
+  // r*: the smallest rank whose running page count reaches k (every wave
+  // finds it itself: no barrier)
+  int run = 0, rstar = k - 1, need = 0;
+  for (int r0 = 0; r0 < k; r0 += 64) {
+    const int r = r0 + lane;
+    const int c = r < k ? (int)lvl[r] : 0;
+    const int incl = run + wave_incl_scan(c);
+    const uint64_t hit = __ballot(r < k && incl >= k);
+    if (hit) {
+      const int src = (int)__builtin_ctzll(hit);
+      rstar = r0 + src;
+      need = k - (__shfl(incl, src) - __shfl(c, src));
+      break;
+    }
+    run = __shfl(incl, 63);
+  }
+  const uint32_t thr1 = (uint32_t)(k - rstar);
+  auto key_l = [&](int p) -> uint32_t {
+    const uint32_t v = level[p];
+    return v == 0xffffffffu ? 0u : (uint32_t)k - v / (uint32_t)G;
+  };
+  pack_selected<NT>(key_l, num_pages, false, thr1, need, wave_cnt, emit);
+}
+
 // LDS words of the candidate lists (page, key, rank) of a group of G > 1
 // query heads: all G lists at once (`concurrent`), else one list at a time.
 __host__ __device__ constexpr int group_list_words(int G, int k, bool concurrent = true) {
@@ -517,6 +656,28 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
       int kk[G];
       radix_threshold_group<NT, kBits, G>(key_gp, num_pages, k, ghist, thr, kk);
       EKV_CSTAMP(12);
+      // 16-bit keys: each head's candidates (keys >= its threshold) are
+      // sorted in LDS instead of packed in page order and ranked pairwise,
+      // and the levels are counted instead of radix-selected
+      if constexpr (kBits == 16 && NT >= 1024) {
+        const int c1 = next_pow2_int(k);
+        const int C2 = (2 * c1 <= 3 * k) ? 2 * c1 : c1;
+        int cmax = 0;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          cmax = max(cmax, k - kk[g] + (int)ghist[kPasses - 1][g][thr[g] & 255u]);
+        if (cmax <= C2 && G * C2 <= list_words && G * C2 <= NT && k <= kPasses * G * 256 &&
+            num_pages <= kGroupSortedPages && C2 >= 4) {
+          group_select_sorted<NT, G>(key_gp, num_pages, k, thr, C2, lds_list, level,
+                                     &ghist[0][0][0], gwave_cnt, wave_cnt, emit_out);
+          if (tid == 0 && last_page >= 0) {
+            if (out) out[k] = last_page;
+            if (lds_out) lds_out[k] = last_page;
+          }
+          EKV_CSTAMP(4);
+          return;
+        }
+      }
       pack_selected_group<NT, G>(key_gp, num_pages, thr, kk, gwave_cnt,
                                  [&](int g, int slot, int p, uint32_t key) {
                                    list_page[g * k + slot] = (uint32_t)p;

@@ -156,6 +156,28 @@ def test_topk_ties_and_edges(dtype):
         assert (got[:, :, k] == P).all()
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("G", [2, 4, 8])
+def test_topk_gqa_ties(dtype, G):
+    """GQA page tables (best rank over the group) on tie-heavy scores: every
+    head's top-k breaks ties toward the lower page, and so does the final
+    selection over levels (compared with the oracle's policy)."""
+    K = _K()
+    _case(test="topk_gqa_ties", dtype=dtype, G=G)
+    rng = np.random.default_rng(40 + G)
+    B, Hkv, P = 2, 2, 1500
+    H = Hkv * G
+    s = O.round_to(np.round(rng.standard_normal((B, H, P)) * 3) / 4, dtype)
+    sd = to_dev(s, dtype)
+    for k in (1, 7, 64, 100, 128, 300, 1499):
+        out = K.topk_pages(sd, k, Hkv, last_page=P)
+        torch.cuda.synchronize()
+        got = to_np(out).astype(np.int64)
+        ref = O.topk_gqa_pages(s, Hkv, k)
+        np.testing.assert_array_equal(got[:, :, :k], ref, err_msg=f"k={k}")
+        assert (got[:, :, k] == P).all()
+
+
 # ---------------------------------------------------------------------------
 # a6 / a13 paged decode
 # ---------------------------------------------------------------------------
