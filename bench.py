@@ -34,8 +34,8 @@ HBM_PEAK_GBS = 8000.0
 def _args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--steps", type=int, default=1000)
+    p.add_argument("--warmup", type=int, default=50)
     p.add_argument("--batch", type=int, default=8)
     p.add_argument("--heads", type=int, default=32)
     p.add_argument("--kv-heads", type=int, default=None)
