@@ -30,32 +30,33 @@ SIGNATURES = {
     "ekv_build_id": (ctypes.c_char_p, []),
     "ekv_page_stats": (I, [P, I64, I64, I64, P, P, P, P, I64, I64, I64, I, I, I, I, P, I, I, I, I,
                            P]),
-    "ekv_append": (I, [P, P, I64, I64, P, P, I64, I64, I64, P, P, P, P, I64, I64, I64,
-                       I, I, I, I, P, I, I, P]),
-    "ekv_page_criticality": (I, [P, I64, I64, P, P, I64, I64, I64, P, P, I, I, I, I, I, I, I, I,
-                                 I, I, P, P, I64, I64, I, P]),
+    "ekv_append": (I, [P, P, I64, I64, P, P, I64, I64, I64, P, P, P, P, I64, I64, I64, I, I, I, I,
+                       P, P, I64, I, I, I, P]),
+    "ekv_page_criticality": (I, [P, I64, I64, P, P, I64, I64, I64, P, P, I, I, I, I, I, I, I, I, I,
+                                 I, P, P, I64, I64, I, P]),
     "ekv_topk_pages": (I, [P, I, I, I, I, I, I, P, I64, I64, I, P]),
     "ekv_decode_workspace_bytes": (I64, [I, I, I, I, I, I]),
-    "ekv_paged_entmax_decode": (I, [P, I64, I64, P, P, I64, I64, I64, I64, P, I64, I64, I,
-                                    P, I64, I64, P, P, P, P, I, I, P, I64, I64, F, F, I, I, I, I,
-                                    I, I, I, P, I64, I, P]),
+    "ekv_paged_entmax_decode": (I, [P, I64, I64, P, P, I64, I64, I64, I64, P, I64, I, P, I64, I64,
+                                    I, P, I64, I64, P, P, P, P, I, I, P, I64, I64, F, F, I, I, I,
+                                    I, I, I, I, P, I64, I, P]),
     "ekv_topk_paged_entmax_decode": (I, [P, I64, I64, P, P, I64, I64, I64, P, I, I, I, I, I, P, P,
-                                         I64, I64, I64, I64, P, I64, I64, P, I64, I64, P, P, P,
-                                         P, I, P, I64, I64, F, F, I, I, I, I, I, I, I, P, I64,
-                                         I, P]),
-    "ekv_topk_paged_entmax_decode_noalloc": (I, [P, I64, I64, P, P, I64, I64, I64, P, I, I, I,
-                                                 I, I, P, P, I64, I64, I64, I64, P, I64, I64, P,
-                                                 I64, I64, P, P, P, P, I, P, I64, I64, F, F, I,
-                                                 I, I, I, I, I, I, I, P]),
+                                         I64, I64, I64, I64, P, I64, I, P, I64, I64, P, I64, I64,
+                                         P, P, P, P, I, P, I64, I64, F, F, I, I, I, I, I, I, I, P,
+                                         I64, I, P]),
+    "ekv_topk_paged_entmax_decode_noalloc": (I, [P, I64, I64, P, P, I64, I64, I64, P, I, I, I, I,
+                                                 I, P, P, I64, I64, I64, I64, P, I64, I, P, I64,
+                                                 I64, P, I64, I64, P, P, P, P, I, P, I64, I64, F,
+                                                 F, I, I, I, I, I, I, I, I, P]),
     "ekv_gaussian_workspace_bytes": (I64, [I, I, I, I, I, I]),
-    "ekv_gaussian_page_stats": (I, [P, I64, I64, P, P, I64, I64, I64, I, P, I, I, P, P, P, P, P,
-                                    P, P, F, I, I, F, P, I, I, I, I, P, I64, I, P]),
-    "ekv_gaussian_moments": (I, [P, I64, I64, P, P, I64, I64, I64, I, P, I, I, I, P, P, P, I, I,
-                                 I, I, P, I64, I, P]),
+    "ekv_gaussian_page_stats": (I, [P, I64, I64, P, P, I64, I64, I64, I, P, I, I, P, P, P, P, P, P,
+                                    P, F, I, I, F, P, I, I, I, I, P, I64, I, P]),
+    "ekv_gaussian_moments": (I, [P, I64, I64, P, P, I64, I64, I64, I, P, I, I, I, P, P, P, I, I, I,
+                                 I, P, I64, I, P]),
     "ekv_gaussian_paged_entmax_decode": (I, [P, I64, P, P, I, I, P, P, P, P, P, I, I, I, F, I, F,
                                              F, F, F, F, P, I64, I64, P, P, P, I, P, F, F, P, P,
-                                             I64, I64, P, P, I64, I64, I64, I64, P, P, P, P, I, I,
-                                             P, I64, I64, F, F, I, I, I, I, I, I, P, I64, I, P]),
+                                             I64, I64, P, P, I64, I64, I64, I64, P, I64, I, P, P,
+                                             P, P, I, I, P, I64, I64, F, F, I, I, I, I, I, I, P,
+                                             I64, I, P]),
     "ekv_tau_single_gaussian": (I, [P, P, P, I, I, F, I, F, P]),
     "ekv_tau_page_mixture": (I, [P, P, P, I, I, F, F, I, F, P, I, I, P]),
     "ekv_select_gaussian_pack": (I, [P, P, P, P, I, I, I, I, I, F, I, F, F, F, F, F, P, I64, I64,
@@ -63,13 +64,13 @@ SIGNATURES = {
     "ekv_tau_clamp": (I, [P, P, P, P, I64, I64, I, P, I64, I64, P, P, I, I, I, I, F, F, F, P]),
     "ekv_cache_seqlens_from_counts": (I, [P, P, I, I, I, P]),
     "ekv_dense_decode_workspace_bytes": (I64, [I, I, I64]),
-    "ekv_dense_entmax_decode": (I, [P, I64, I64, P, P, I64, I64, I64, I64, P, P, I64, I64, P, P,
-                                    P, I, P, I64, I64, F, F, I, I, I, I, P, I64, I, P]),
+    "ekv_dense_entmax_decode": (I, [P, I64, I64, P, P, I64, I64, I64, I64, P, P, I64, I64, P, P, P,
+                                    I, P, I64, I64, F, F, I, I, I, I, P, I64, I, P]),
     "ekv_entmax_rows_forward": (I, [P, I64, P, I64, I64, I, F, P, I, P]),
     "ekv_entmax_rows_backward": (I, [P, I64, P, I64, P, I64, I64, I, F, I, P]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib = None

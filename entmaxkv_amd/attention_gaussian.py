@@ -93,7 +93,7 @@ def sparse_attention_decode_gaussian_aware_entmax(
     last_page_size = (seq_len - (math.ceil(seq_len / page_size) - 1) * page_size
                       if seq_len > page_size else seq_len)
     do_clamp = needs_tau and clamp_tau
-    sb = kv_cache._get_select_buffers(batch, num_heads, kv_cache._k.shape[1], num_pages,
+    sb = kv_cache._get_select_buffers(batch, num_heads, kv_cache.num_kv_heads, num_pages,
                                       q.device)
     workspace = kv_cache.get_paged_decode_workspace(
         batch, num_heads, head_dim, splits, 16, q.dtype, q.device,
@@ -108,8 +108,9 @@ def sparse_attention_decode_gaussian_aware_entmax(
             else:
                 tau_correction_iters = 1 if alibi_slopes is None else 2
         iters = tau_correction_iters
+    kc, vc, rows, blocks = kv_cache.kv_operands()
     K.gaussian_paged_entmax_decode(
-        q, kv_cache._k, kv_cache._v, out, buf, pages_for_stats=pages_for_stats,
+        q, kc, vc, out, buf, pages_for_stats=pages_for_stats,
         num_pages=num_pages, n_tokens=seq_len_for_stats, page_size=page_size, alpha=alpha,
         tau_hat_given=tau_hat_given, safety_margin_z=None, max_quantile=None,
         threshold_excess_margin_fraction=threshold_excess_margin_fraction,
@@ -118,8 +119,8 @@ def sparse_attention_decode_gaussian_aware_entmax(
         tau_clamped=sb["tau_clamped"] if do_clamp else None,
         clamp_quantile=tau_clamp_page_max_quantile, effective=sb["effective"],
         tau_out=workspace.taus, tau_mode=dec_mode, iters=iters, workspace=workspace,
-        alibi_slopes=alibi_slopes, q_seqlens=q_seqlens, kv_rows=kv_cache.kv_capacity,
-        seq_lens=seq_lens)
+        alibi_slopes=alibi_slopes, q_seqlens=q_seqlens, kv_rows=rows,
+        seq_lens=seq_lens, blocks=blocks)
     kv_cache.record_gaussian_selection(gaussian_stats, sb, do_clamp)
     if tau_mode != "exact":
         gaussian_stats["tau_final"] = workspace.taus

@@ -40,7 +40,7 @@ def sparse_attention_decode_paged(
     ``q_seqlens`` defaults to the sequence lengths.
     """
     batch, num_heads, _, head_dim = q.shape
-    num_kv_heads = kv_cache.k_cache.shape[1]
+    num_kv_heads = kv_cache.num_kv_heads
 
     if append_cache:
         kv_cache.append(k_new, v_new)
@@ -62,10 +62,11 @@ def sparse_attention_decode_paged(
 
     if num_pages_to_select == 0:
         page_indices = kv_cache.select_topk(q, 0, alibi_slopes=alibi_slopes)
+        kc, vc, rows, blocks = kv_cache.kv_operands()
         K.paged_entmax_decode(
-            q, kv_cache._k, kv_cache._v, out, cache_seqlens, page_indices, page_size, alpha,
+            q, kc, vc, out, cache_seqlens, page_indices, page_size, alpha,
             tau_mode=0, iters=niter, tau=None, alibi_slopes=alibi_slopes, q_seqlens=q_seqlens,
-            workspace=workspace, kv_rows=kv_cache.kv_capacity)
+            workspace=workspace, kv_rows=rows, blocks=blocks)
         return out
 
     # criticality + top-k + decode in one launch (two when the shape needs it)
@@ -73,9 +74,10 @@ def sparse_attention_decode_paged(
     page_indices = kv_cache.get_page_indices_buf(batch, num_kv_heads, num_pages_to_select, last)
     scores = kv_cache._get_scores_buf(batch, num_heads, total_pages - 1, q.dtype, q.device)
     kv_cache.last_page_scores = scores
+    kc, vc, rows, blocks = kv_cache.kv_operands()
     K.topk_paged_entmax_decode(
-        q, kv_cache.k_min, kv_cache.k_max, scores, num_pages_to_select, last, kv_cache._k,
-        kv_cache._v, out, page_indices, cache_seqlens, page_size, alpha, niter, seq_len,
+        q, kv_cache.k_min, kv_cache.k_max, scores, num_pages_to_select, last, kc,
+        vc, out, page_indices, cache_seqlens, page_size, alpha, niter, seq_len,
         seq_len - 1, alibi_slopes=alibi_slopes, q_seqlens=q_seqlens, workspace=workspace,
-        kv_rows=kv_cache.kv_capacity, seq_lens=seq_lens)
+        kv_rows=rows, seq_lens=seq_lens, blocks=blocks)
     return out

@@ -76,6 +76,13 @@ struct DecodeArgs {
   const void* v;
   int64_t ksb, ksh, ksr;
   int64_t row_limit;  // rows addressable in each (b, kv head) of K/V
+  // Block pool (null: contiguous cache).  Row r of (b, kv head) then lives in
+  // block block_table[b * btsb + r / page_size] at
+  // block * ksb + kvh * ksh + (r % page_size) * ksr; ids outside [0,
+  // bt_blocks) are skipped like out-of-range page ids.
+  const int32_t* block_table = nullptr;
+  int64_t btsb = 0;
+  int bt_blocks = 0;
   const int32_t* page_indices;
   int64_t pisb, pish;
   int n_slots;
@@ -122,6 +129,18 @@ __device__ __forceinline__ float entmax_weight(float x, float alpha, float c0) {
   if (alpha == 2.0f) return x;
   if (alpha == 1.5f) return x * x;
   return exp2f(log2f(x) * c0);
+}
+
+// Element offset of cache row `row` of (b, kv head) from the K/V base
+// pointer, or -1 when the row lies outside the cache (contiguous rows, or a
+// block of the pool; see DecodeArgs::block_table).
+__device__ __forceinline__ int64_t kv_row_offset(const DecodeArgs& a, int b, int kvh,
+                                                 int64_t row) {
+  if (row < 0 || row >= a.row_limit) return -1;
+  if (!a.block_table) return b * a.ksb + kvh * a.ksh + row * a.ksr;
+  const int blk = a.block_table[b * a.btsb + row / a.page_size];
+  if (blk < 0 || blk >= a.bt_blocks) return -1;
+  return blk * a.ksb + kvh * a.ksh + (row % a.page_size) * a.ksr;
 }
 
 // q * qscale rounded to the storage dtype, kept in the storage format
@@ -212,28 +231,33 @@ __device__ __forceinline__ void score_rows_mfma(const DecodeArgs& a, int b, int 
     q_idx = (a.q_seqlens ? a.q_seqlens[b] : a.cache_seqlens[b * a.csb + kvh * a.csh]) - 1;
     slope = j < G ? a.slopes[h0 + j] * (a.alpha - 1.0f) : 0.f;
   }
-  const T* kh = (const T*)a.k + b * a.ksb + kvh * a.ksh;
+  const T* kbase = (const T*)a.k;
   const bool kpos = a.slopes && a.positions;
   const int ps = a.page_size;
-  constexpr int kNoRow = INT_MIN;
+  // logical cache row of compacted token c (the ALiBi distance)
   auto row_of = [&](int c) -> int {
-    const int page = pages[(c - c_base) / ps];
-    const int64_t row = (int64_t)page * ps + (c % ps);
-    return (page >= 0 && row < a.row_limit) ? (int)row : kNoRow;
+    return pages[(c - c_base) / ps] * ps + (c % ps);
   };
   float rmax = -1.0e6f;
-  // tile t covers tokens c_begin + 16 t .. + 15; wave wid takes tiles wid + W (u + U m)
-  auto fetch = [&](int m, uint4 (&kv)[U][KB]) {
+  // tile t covers tokens c_begin + 16 t .. + 15; wave wid takes tiles wid + W (u + U m).
+  // Lane j (of each 16) resolves token j's row once; the ballot of the
+  // valid ones tells the accumulator lanes (token 4 kq + r) which to mask.
+  auto fetch = [&](int m, uint4 (&kv)[U][KB], uint64_t (&vm)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = c_begin + ((m * U + u) * W + wid) * 16 + j;
-      const int row = c < c_end ? row_of(c) : kNoRow;
-      const T* kr = kh + (int64_t)max(row, 0) * a.ksr + 8 * kq;
+      int64_t off = -1;
+      if (c < c_end) {
+        const int page = pages[(c - c_base) / ps];
+        if (page >= 0) off = kv_row_offset(a, b, kvh, (int64_t)page * ps + (c % ps));
+      }
+      vm[u] = __ballot(off >= 0);
+      const T* kr = kbase + (off >= 0 ? off : 0) + 8 * kq;
 #pragma unroll
       for (int i = 0; i < KB; ++i) kv[u][i] = ld16(kr + 32 * i);
     }
   };
-  auto consume = [&](int m, const uint4 (&kv)[U][KB]) {
+  auto consume = [&](int m, const uint4 (&kv)[U][KB], const uint64_t (&vm)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       ekv_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -245,10 +269,9 @@ __device__ __forceinline__ void score_rows_mfma(const DecodeArgs& a, int b, int 
         for (int r = 0; r < 4; ++r) {
           const int c = t0 + r;
           if (c < c_end) {
-            const int row = row_of(c);
             float s = acc[r];
-            if (row == kNoRow) s = -INFINITY;
-            else if (a.slopes && !kpos) s += slope * (float)(row - q_idx);
+            if (!((vm[u] >> (4 * kq + r)) & 1)) s = -INFINITY;
+            else if (a.slopes && !kpos) s += slope * (float)(row_of(c) - q_idx);
             sc[j * stride + c] = s;
             if (!kpos) rmax = fmaxf(rmax, s);
           }
@@ -259,20 +282,21 @@ __device__ __forceinline__ void score_rows_mfma(const DecodeArgs& a, int b, int 
   const int tiles = c_end > c_begin ? (c_end - c_begin + 15) / 16 : 0;
   const int rounds = (tiles + U * W - 1) / (U * W);
   uint4 kv_a[U][KB], kv_b[U][KB];
-  if (rounds > 0) fetch(0, kv_a);
+  uint64_t vm_a[U], vm_b[U];
+  if (rounds > 0) fetch(0, kv_a, vm_a);
   int r = 0;
   for (; r + 2 < rounds; r += 2) {
-    fetch(r + 1, kv_b);
-    consume(r, kv_a);
-    fetch(r + 2, kv_a);
-    consume(r + 1, kv_b);
+    fetch(r + 1, kv_b, vm_b);
+    consume(r, kv_a, vm_a);
+    fetch(r + 2, kv_a, vm_a);
+    consume(r + 1, kv_b, vm_b);
   }
   if (r + 1 < rounds) {
-    fetch(r + 1, kv_b);
-    consume(r, kv_a);
-    consume(r + 1, kv_b);
+    fetch(r + 1, kv_b, vm_b);
+    consume(r, kv_a, vm_a);
+    consume(r + 1, kv_b, vm_b);
   } else if (r < rounds) {
-    consume(r, kv_a);
+    consume(r, kv_a, vm_a);
   }
   if (kpos && j < G) {
     // explicit key positions: the ALiBi term over the scores this lane wrote
@@ -284,9 +308,11 @@ __device__ __forceinline__ void score_rows_mfma(const DecodeArgs& a, int b, int 
         for (int rr = 0; rr < 4; ++rr) {
           const int c = t0 + rr;
           if (c >= c_end) continue;
-          const int row = row_of(c);
+          const int page = pages[(c - c_base) / ps];
+          const int64_t row = (int64_t)page * ps + (c % ps);
+          const bool valid = page >= 0 && kv_row_offset(a, b, kvh, row) >= 0;
           float s = sc[j * stride + c];
-          if (row != kNoRow) s += slope * (float)(pos[row] - q_idx);
+          if (valid) s += slope * (float)(pos[row] - q_idx);
           sc[j * stride + c] = s;
           rmax = fmaxf(rmax, s);
         }
@@ -327,7 +353,7 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
 #pragma unroll
     for (int g = 0; g < G; ++g) slope[g] = a.slopes[h0 + g] * (a.alpha - 1.0f);
   }
-  const T* kh = (const T*)a.k + b * a.ksb + kvh * a.ksh;
+  const T* kbase = (const T*)a.k;
   const int32_t* kpos = a.slopes && a.positions ? a.positions + b * a.posb + kvh * a.posh : nullptr;
   const int ps = a.page_size;
   constexpr int kNoRow = INT_MIN;
@@ -335,18 +361,24 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
   // are unconditional (an invalid token re-reads row 0 and is masked), so
   // all U of them are in flight together.
   auto fetch = [&](int c0, int (&rows)[U], uint4 (&kv)[U]) {
+    int64_t off[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = c0 + u * SEGS + seg;
       rows[u] = kNoRow;
+      off[u] = 0;  // an invalid token re-reads the cache's first element
       if (c < c_end) {
         const int page = pages[(c - c_base) / ps];
         const int64_t row = (int64_t)page * ps + (c % ps);
-        rows[u] = (page >= 0 && row < a.row_limit) ? (int)row : kNoRow;
+        const int64_t o = page >= 0 ? kv_row_offset(a, b, kvh, row) : -1;
+        if (o >= 0) {
+          rows[u] = (int)row;
+          off[u] = o;
+        }
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) kv[u] = ld16(kh + (int64_t)max(rows[u], 0) * a.ksr + col);
+    for (int u = 0; u < U; ++u) kv[u] = ld16(kbase + off[u] + col);
   };
   auto consume = [&](int c0, const int (&rows)[U], const uint4 (&kv)[U]) {
 #pragma unroll
@@ -398,7 +430,7 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
     for (int c = c_begin + seg; c < c_end; c += SEGS) {
       const int page = pages[(c - c_base) / ps];
       const int64_t row = (int64_t)page * ps + (c % ps);
-      const bool valid = page >= 0 && row < a.row_limit;
+      const bool valid = page >= 0 && kv_row_offset(a, b, kvh, row) >= 0;
       const float bias = valid ? (float)(kpos[valid ? row : 0] - q_idx) : 0.f;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -790,7 +822,7 @@ struct HeadShared {
   int (*hist)[kBins];
   float4* part;  // [2][kWaves] reduction partials
   float* s_tau;
-  int* sup_row;  // [sup_chunk(G)]
+  int* sup_row;  // [sup_chunk(G)] V rows of the support (rows of ksr elements from the base)
   float* sup_p;  // [G][sup_chunk(G)]
   int* flag_cnt;
   float* red;    // [kWaves][D]
@@ -896,7 +928,7 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
   const float c0 = 1.0f / (alpha - 1.0f);
   const int seg = tid / LPR;
   const int col = (tid % LPR) * VEC;
-  const T* vh = (const T*)a.v + b * a.ksb + kvh * a.ksh;
+  const T* vbase = (const T*)a.v;
   float acc[G][VEC];
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -953,8 +985,10 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
             r = (int64_t)pg * ps + (c % ps);
             r = (pg >= 0 && r < a.row_limit) ? r : -1;
           }
-          row[j] = (int)r;
-          if (r < 0) any[j] = false;
+          // the row's place in V, in rows of ksr elements from the base
+          const int64_t o = r >= 0 ? kv_row_offset(a, b, kvh, r) : -1;
+          row[j] = (int)(o / a.ksr);
+          if (o < 0) any[j] = false;
         }
       }
       m[j] = __ballot(any[j]);
@@ -989,7 +1023,7 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
       uint4 x[R];
 #pragma unroll
       for (int r = 0; r < R; ++r)
-        x[r] = ld16(vh + (int64_t)sh.sup_row[min(j0 + r * SEGS, nsup - 1)] * a.ksr + col);
+        x[r] = ld16(vbase + (int64_t)sh.sup_row[min(j0 + r * SEGS, nsup - 1)] * a.ksr + col);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int j = j0 + r * SEGS;

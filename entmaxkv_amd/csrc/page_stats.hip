@@ -106,7 +106,8 @@ template <typename T, int LPR>
 __global__ __launch_bounds__(64) void append_kernel(
     const T* __restrict__ k_new, const T* __restrict__ v_new, int64_t nsb, int64_t nsh, T* k, T* v,
     int64_t ksb, int64_t ksh, int64_t ksr, StatsPtrs st, int64_t ssb, int64_t ssh, int64_t ssp,
-    int B, int Hkv, const int* __restrict__ pos_per_batch, int pos_scalar, int page_size) {
+    int B, int Hkv, const int* __restrict__ pos_per_batch, int pos_scalar, int page_size,
+    const int32_t* __restrict__ block_table, int64_t btsb, int bt_blocks) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int SPB = 64 / LPR;
   const int seg = threadIdx.x / LPR;
@@ -120,6 +121,15 @@ __global__ __launch_bounds__(64) void append_kernel(
   const T* vn = v_new + b * nsb + h * nsh;
   T* kh = k + b * ksb + h * ksh;
   T* vh = v + b * ksb + h * ksh;
+  if (block_table) {
+    // every row of this page lies in one block of the pool: kh + r * ksr
+    // addresses row r of the page for r in [page * ps, pos]
+    const int blk = block_table[b * btsb + pos / page_size];
+    if (blk < 0 || blk >= bt_blocks) return;
+    const int64_t shift = (int64_t)blk * ksb + h * ksh - (int64_t)(pos / page_size) * page_size * ksr;
+    kh = k + shift;
+    vh = v + shift;
+  }
   Vec<T> kx, vx;
   kx.load(kn + col);
   vx.load(vn + col);
@@ -200,12 +210,13 @@ int launch_stats(const void* k, int64_t ksb, int64_t ksh, int64_t ksr, StatsPtrs
 template <typename T, int LPR>
 int launch_append(const void* kn, const void* vn, int64_t nsb, int64_t nsh, void* k, void* v,
                   int64_t ksb, int64_t ksh, int64_t ksr, StatsPtrs st, int64_t ssb, int64_t ssh,
-                  int64_t ssp, int B, int Hkv, const int* pos_b, int pos, int ps, hipStream_t s) {
+                  int64_t ssp, int B, int Hkv, const int* pos_b, int pos, int ps,
+                  const int32_t* bt, int64_t btsb, int bt_blocks, hipStream_t s) {
   constexpr int SPB = 64 / LPR;
   dim3 grid((B * Hkv + SPB - 1) / SPB);
   hipLaunchKernelGGL((append_kernel<T, LPR>), grid, dim3(64), 0, s, (const T*)kn, (const T*)vn,
                      nsb, nsh, (T*)k, (T*)v, ksb, ksh, ksr, st, ssb, ssh, ssp, B, Hkv, pos_b, pos,
-                     ps);
+                     ps, bt, btsb, bt_blocks);
   return check_launch("append_kernel");
 }
 
@@ -241,11 +252,14 @@ extern "C" int ekv_append(const void* k_new, const void* v_new, int64_t new_stri
                           int64_t k_stride_h, int64_t k_stride_row, void* kmin, void* kmax,
                           void* kmean, void* kstd, int64_t s_stride_b, int64_t s_stride_h,
                           int64_t s_stride_page, int B, int Hkv, int D, int pos,
-                          const int32_t* pos_per_batch, int page_size, int dtype, void* stream) {
+                          const int32_t* pos_per_batch, const int32_t* block_table,
+                          int64_t bt_stride_b, int bt_blocks, int page_size, int dtype,
+                          void* stream) {
   EKV_REQUIRE(k_new && v_new && k && v && kmin && kmax && kmean && kstd,
               "ekv_append: null pointer");
   EKV_REQUIRE(B > 0 && Hkv > 0 && page_size > 0, "ekv_append: bad sizes");
   EKV_REQUIRE(pos_per_batch || pos >= 0, "ekv_append: negative position");
+  EKV_REQUIRE(!block_table || bt_blocks > 0, "ekv_append: a block table needs bt_blocks > 0");
   StatsPtrs st{kmin, kmax, kmean, kstd};
   hipStream_t s = (hipStream_t)stream;
   return dispatch_dtype(dtype, [&](auto tv) {
@@ -253,7 +267,8 @@ extern "C" int ekv_append(const void* k_new, const void* v_new, int64_t new_stri
     return dispatch_lpr<T>(D, [&](auto lpr) {
       return launch_append<T, decltype(lpr)::value>(
           k_new, v_new, new_stride_b, new_stride_h, k, v, k_stride_b, k_stride_h, k_stride_row, st,
-          s_stride_b, s_stride_h, s_stride_page, B, Hkv, pos_per_batch, pos, page_size, s);
+          s_stride_b, s_stride_h, s_stride_page, B, Hkv, pos_per_batch, pos, page_size,
+          block_table, bt_stride_b, bt_blocks, s);
     });
   });
 }

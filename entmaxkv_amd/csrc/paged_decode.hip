@@ -10,6 +10,27 @@ using namespace ekv::dec;
 
 namespace {
 
+// The block pool of a cache that is not contiguous per (b, kv head): see
+// DecodeArgs::block_table.
+struct KvBlocks {
+  const int32_t* table = nullptr;
+  int64_t stride_b = 0;
+  int count = 0;
+};
+
+// Checks shared by the decode entry points on the K/V addressing: support
+// rows are kept as offsets in rows of kv_stride_row elements, and a block
+// table needs a pool.
+int check_kv_layout(const char* what, int64_t kv_stride_b, int64_t kv_stride_h,
+                    int64_t kv_stride_row, const KvBlocks& blocks) {
+  EKV_REQUIRE(kv_stride_row > 0 && kv_stride_b % kv_stride_row == 0 &&
+                  kv_stride_h % kv_stride_row == 0,
+              "%s: K/V strides must be multiples of the row stride", what);
+  EKV_REQUIRE(!blocks.table || (blocks.count > 0 && blocks.stride_b >= 0),
+              "%s: a block table needs bt_blocks > 0", what);
+  return EKV_OK;
+}
+
 template <typename F>
 int dispatch_group(int G, F&& f) {
   switch (G) {
@@ -28,8 +49,12 @@ DecodeArgs make_decode_args(
     const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
     const int32_t* q_seqlens, const float* alibi_slopes, const float* tau_in, float* tau,
     int tau_mode, int iters, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha,
-    float qscale, int page_size, int H, int Hkv, int splits, int max_tokens, void* workspace) {
+    float qscale, int page_size, int H, int Hkv, int splits, int max_tokens, void* workspace,
+    const KvBlocks& blocks = KvBlocks{}) {
   DecodeArgs a;
+  a.block_table = blocks.table;
+  a.btsb = blocks.stride_b;
+  a.bt_blocks = blocks.count;
   a.q = q;
   a.qsb = q_stride_b;
   a.qsh = q_stride_h;
@@ -94,7 +119,8 @@ static int paged_decode(
     int tau_mode, int iters, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha,
     float qscale, int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens,
     void* workspace, int64_t workspace_bytes, int dtype, void* stream, bool force_split,
-    const int32_t* positions = nullptr, int64_t pos_stride_b = 0, int64_t pos_stride_h = 0) {
+    const int32_t* positions = nullptr, int64_t pos_stride_b = 0, int64_t pos_stride_h = 0,
+    const KvBlocks& blocks = KvBlocks{}) {
   EKV_REQUIRE(q && k && v && page_indices && cache_seqlens && tau && out && workspace,
               "ekv_paged_entmax_decode: null pointer");
   EKV_REQUIRE(B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0, "ekv_paged_entmax_decode: bad heads");
@@ -106,12 +132,15 @@ static int paged_decode(
   EKV_REQUIRE(alpha > 1.0f, "ekv_paged_entmax_decode: alpha must be > 1");
   EKV_REQUIRE(workspace_bytes >= ekv_decode_workspace_bytes(B, H, Hkv, D, splits, max_tokens),
               "ekv_paged_entmax_decode: workspace too small");
+  if (int rc = check_kv_layout("ekv_paged_entmax_decode", kv_stride_b, kv_stride_h,
+                               kv_stride_row, blocks))
+    return rc;
   DecodeArgs a = make_decode_args(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h,
                                   kv_stride_row, kv_rows, page_indices, pi_stride_b, pi_stride_h,
                                   n_slots, cache_seqlens, cs_stride_b, cs_stride_h, q_seqlens,
                                   alibi_slopes, tau_in, tau, tau_mode, iters, out, out_stride_b,
                                   out_stride_h, alpha, qscale, page_size, H, Hkv, splits,
-                                  max_tokens, workspace);
+                                  max_tokens, workspace, blocks);
   a.positions = positions;
   a.posb = pos_stride_b;
   a.posh = pos_stride_h;
@@ -132,6 +161,7 @@ static int paged_decode(
 extern "C" int ekv_paged_entmax_decode(
     const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k, const void* v,
     int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+    const int32_t* block_table, int64_t bt_stride_b, int bt_blocks,
     const int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h, int n_slots,
     const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
     const int32_t* q_seqlens, const float* alibi_slopes, const float* tau_in, float* tau,
@@ -142,7 +172,8 @@ extern "C" int ekv_paged_entmax_decode(
                       kv_rows, page_indices, pi_stride_b, pi_stride_h, n_slots, cache_seqlens,
                       cs_stride_b, cs_stride_h, q_seqlens, alibi_slopes, tau_in, tau, tau_mode,
                       iters, out, out_stride_b, out_stride_h, alpha, qscale, page_size, B, H, Hkv,
-                      D, splits, max_tokens, workspace, workspace_bytes, dtype, stream, false);
+                      D, splits, max_tokens, workspace, workspace_bytes, dtype, stream, false,
+                      nullptr, 0, 0, KvBlocks{block_table, bt_stride_b, bt_blocks});
 }
 
 extern "C" int ekv_topk_paged_entmax_decode(
@@ -150,12 +181,14 @@ extern "C" int ekv_topk_paged_entmax_decode(
     int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, void* scores, int num_pages,
     int seq_len, int q_pos, int k_select, int last_page, const void* k, const void* v,
     int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+    const int32_t* block_table, int64_t bt_stride_b, int bt_blocks,
     int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h,
     const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
     const int32_t* q_seqlens, const float* alibi_slopes, const int32_t* seq_lens, float* tau,
     int niter, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale,
     int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens, void* workspace,
     int64_t workspace_bytes, int dtype, void* stream) {
+  const KvBlocks blocks{block_table, bt_stride_b, bt_blocks};
   EKV_REQUIRE(q && kmin && kmax && scores && k && v && page_indices && cache_seqlens && tau &&
                   out && workspace,
               "ekv_topk_paged_entmax_decode: null pointer");
@@ -167,6 +200,9 @@ extern "C" int ekv_topk_paged_entmax_decode(
               "ekv_topk_paged_entmax_decode: bad decode parameters");
   EKV_REQUIRE(workspace_bytes >= ekv_decode_workspace_bytes(B, H, Hkv, D, splits, max_tokens),
               "ekv_topk_paged_entmax_decode: workspace too small");
+  if (int rc = check_kv_layout("ekv_topk_paged_entmax_decode", kv_stride_b, kv_stride_h,
+                               kv_stride_row, blocks))
+    return rc;
   const int n_slots = k_select + (last_page >= 0 ? 1 : 0);
   const int G = H / Hkv;
   auto two_launches = [&]() {
@@ -180,7 +216,7 @@ extern "C" int ekv_topk_paged_entmax_decode(
                         cs_stride_b, cs_stride_h, q_seqlens, alibi_slopes, nullptr, tau, 0, niter,
                         out, out_stride_b, out_stride_h, alpha, qscale, page_size, B, H, Hkv, D,
                         splits, max_tokens, workspace, workspace_bytes, dtype, stream,
-                        seq_lens != nullptr);
+                        seq_lens != nullptr, nullptr, 0, 0, blocks);
   };
   // one launch when every head fills a workgroup and its keys, page table and
   // scores stay in LDS; otherwise criticality+top-k, then the decode
@@ -193,7 +229,7 @@ extern "C" int ekv_topk_paged_entmax_decode(
                                   n_slots, cache_seqlens, cs_stride_b, cs_stride_h, q_seqlens,
                                   alibi_slopes, nullptr, tau, 0, niter, out, out_stride_b,
                                   out_stride_h, alpha, qscale, page_size, H, Hkv, splits,
-                                  max_tokens, workspace);
+                                  max_tokens, workspace, blocks);
   a.stage_cap = tokens;
   a.scores_ready = 0;
   SelectArgs t;
@@ -244,11 +280,13 @@ extern "C" int ekv_gaussian_paged_entmax_decode(
     float* tau_floor, int32_t* cache_seqlens, int last_page_size, float* tau_clamped,
     float z_clamp, float eps, float* effective_margins, const void* q, int64_t q_stride_b,
     int64_t q_stride_h, const void* k, const void* v, int64_t kv_stride_b, int64_t kv_stride_h,
-    int64_t kv_stride_row, int64_t kv_rows, const int32_t* q_seqlens, const float* alibi_slopes,
+    int64_t kv_stride_row, int64_t kv_rows, const int32_t* block_table, int64_t bt_stride_b,
+    int bt_blocks, const int32_t* q_seqlens, const float* alibi_slopes,
     const int32_t* seq_lens, float* tau, int tau_mode, int iters, void* out,
     int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale, int page_size, int B,
     int H, int Hkv, int D, int max_tokens, void* workspace, int64_t workspace_bytes, int dtype,
     void* stream) {
+  const KvBlocks blocks{block_table, bt_stride_b, bt_blocks};
   EKV_REQUIRE(moments_workspace && mu_p && sigma_p && mu_g && sigma_g && mean_var && var_means &&
                   tau_hat && page_indices && counts && tau_floor && cache_seqlens && q && k &&
                   v && tau && out && workspace,
@@ -268,6 +306,9 @@ extern "C" int ekv_gaussian_paged_entmax_decode(
               "ekv_gaussian_paged_entmax_decode: bad decode parameters");
   EKV_REQUIRE(workspace_bytes >= ekv_decode_workspace_bytes(B, H, Hkv, D, 1, max_tokens),
               "ekv_gaussian_paged_entmax_decode: workspace too small");
+  if (int rc = check_kv_layout("ekv_gaussian_paged_entmax_decode", kv_stride_b, kv_stride_h,
+                               kv_stride_row, blocks))
+    return rc;
   hipStream_t s = (hipStream_t)stream;
   const int G = H / Hkv;
   const float* tau_start = tau_clamped ? tau_clamped : tau_hat;
@@ -289,14 +330,14 @@ extern "C" int ekv_gaussian_paged_entmax_decode(
                         Hkv, 1, q_seqlens, alibi_slopes, tau_start, tau, tau_mode, iters, out,
                         out_stride_b, out_stride_h, alpha, qscale, page_size, B, H, Hkv, D,
                         splits_for(max_tokens), max_tokens, workspace, workspace_bytes, dtype,
-                        stream, seq_lens != nullptr);
+                        stream, seq_lens != nullptr, nullptr, 0, 0, blocks);
   }
   DecodeArgs a = make_decode_args(q, q_stride_b, q_stride_h, k, v, kv_stride_b, kv_stride_h,
                                   kv_stride_row, kv_rows, page_indices, pi_stride_b, pi_stride_h,
                                   num_pages, cache_seqlens, Hkv, 1, q_seqlens, alibi_slopes,
                                   tau_start, tau, tau_mode, iters, out, out_stride_b,
                                   out_stride_h, alpha, qscale, page_size, H, Hkv, 1, max_tokens,
-                                  workspace);
+                                  workspace, blocks);
   a.scores_ready = 0;
   GaussArgs f;
   gauss::SelectArgs& sel = f.sel;

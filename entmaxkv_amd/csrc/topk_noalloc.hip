@@ -53,6 +53,7 @@ extern "C" int ekv_topk_paged_entmax_decode_noalloc(
     int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, void* scores, int num_pages,
     int seq_len, int q_pos, int k_select, int last_page, const void* k, const void* v,
     int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+    const int32_t* block_table, int64_t bt_stride_b, int bt_blocks,
     int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h,
     const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
     const int32_t* q_seqlens, const float* alibi_slopes, const int32_t* seq_lens, float* tau,
@@ -73,7 +74,7 @@ extern "C" int ekv_topk_paged_entmax_decode_noalloc(
   return ekv_topk_paged_entmax_decode(
       q, q_stride_b, q_stride_h, kmin, kmax, s_stride_b, s_stride_h, s_stride_page, scores,
       num_pages, seq_len, q_pos, k_select, last_page, k, v, kv_stride_b, kv_stride_h,
-      kv_stride_row, kv_rows, page_indices, pi_stride_b, pi_stride_h, cache_seqlens, cs_stride_b,
+      kv_stride_row, kv_rows, block_table, bt_stride_b, bt_blocks, page_indices, pi_stride_b, pi_stride_h, cache_seqlens, cs_stride_b,
       cs_stride_h, q_seqlens, alibi_slopes, seq_lens, tau, niter, out, out_stride_b, out_stride_h,
       alpha, qscale, page_size, B, H, Hkv, D, splits, max_tokens, ws, kScratchBytes, dtype,
       stream);

@@ -11,6 +11,8 @@ from __future__ import annotations
 import math
 from statistics import NormalDist
 
+from typing import NamedTuple
+
 import torch
 
 from ._lib import call, dtype_code, lib, ptr, require_gpu, stream_ptr
@@ -26,6 +28,23 @@ def _row_major_d(t: torch.Tensor, name: str) -> torch.Tensor:
     ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
           and all(s % vec == 0 for s in t.stride()[:-1]))
     return t if ok else t.contiguous()
+
+
+class KVBlocks(NamedTuple):
+    """A block pool layout of K/V: ``table`` [B, pages] int32 maps a
+    sequence's page to a block of the pool [num_blocks, Hkv, page_size, D]
+    (no counterpart in the reference, whose cache is contiguous)."""
+    table: torch.Tensor
+    num_blocks: int
+
+
+def _bt_args(blocks: "KVBlocks | None"):
+    if blocks is None:
+        return (None, 0, 0)
+    t = blocks.table
+    if t.dtype != torch.int32 or t.dim() != 2 or t.stride(1) != 1 or not t.is_cuda:
+        raise ValueError("block table must be a row-major int32 [B, pages] GPU tensor")
+    return (t.data_ptr(), t.stride(0), int(blocks.num_blocks))
 
 
 def choose_splits(max_tokens: int) -> int:
@@ -61,10 +80,12 @@ def page_stats(k: torch.Tensor, kmin, kmax, kmean, kstd, seq_len: int, page_size
 
 
 def append_token(k_new, v_new, k, v, kmin, kmax, kmean, kstd, pos: int, page_size: int,
-                 pos_per_batch: torch.Tensor | None = None) -> None:
-    """Write row ``pos`` of K/V and recompute its page statistics, in place."""
+                 pos_per_batch: torch.Tensor | None = None,
+                 blocks: KVBlocks | None = None) -> None:
+    """Write row ``pos`` of K/V and recompute its page statistics, in place
+    (``k``/``v`` the block pool when ``blocks`` is given)."""
     require_gpu(k_new, v_new, k)
-    B, Hkv, _, D = k.shape
+    B, Hkv, D = kmin.shape[0], k.shape[1], k.shape[3]
     k_new = _row_major_d(k_new, "k_new")
     v_new = _row_major_d(v_new, "v_new")
     if k_new.stride() != v_new.stride():
@@ -74,7 +95,8 @@ def append_token(k_new, v_new, k, v, kmin, kmax, kmean, kstd, pos: int, page_siz
          k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
          kmin.data_ptr(), kmax.data_ptr(), kmean.data_ptr(), kstd.data_ptr(),
          kmin.stride(0), kmin.stride(1), kmin.stride(2), B, Hkv, D, pos,
-         ptr(pos_per_batch), page_size, dtype_code(k.dtype), stream_ptr(k.device))
+         ptr(pos_per_batch), *_bt_args(blocks), page_size, dtype_code(k.dtype),
+         stream_ptr(k.device))
 
 
 # ---------------------------------------------------------------------------
@@ -166,11 +188,14 @@ def _cache_seqlens_2d(cache_seqlens, batch, num_kv_heads):
 def paged_entmax_decode(q, k_cache, v_cache, out, cache_seqlens, page_indices, page_size,
                         alpha, tau_mode: int, iters: int, tau: torch.Tensor | None,
                         alibi_slopes=None, q_seqlens=None, workspace: DecodeWorkspace | None = None,
-                        kv_rows: int | None = None, tau_in: torch.Tensor | None = None):
+                        kv_rows: int | None = None, tau_in: torch.Tensor | None = None,
+                        blocks: KVBlocks | None = None):
     """Shared launcher of the exact-tau (tau_mode 0) and given-tau (1) decode.
 
     The final tau goes to ``tau`` (the workspace's buffer when None); in
     given-tau mode the start value is read from ``tau_in`` (default: ``tau``).
+    With ``blocks``, ``k_cache``/``v_cache`` are the block pool
+    [num_blocks, Hkv, page_size, D] and ``kv_rows`` bounds a sequence's rows.
     """
     require_gpu(q, k_cache, v_cache, out, page_indices)
     batch, nheads, q_len, dim = q.shape
@@ -178,7 +203,9 @@ def paged_entmax_decode(q, k_cache, v_cache, out, cache_seqlens, page_indices, p
     assert q_len == 1
     assert page_indices.dtype == torch.int32
     assert nheads % num_kv_heads == 0, "Query heads must be divisible by KV heads"
-    assert tuple(v_cache.shape[:2]) == (batch, num_kv_heads), "K/V cache head shapes must match"
+    assert tuple(v_cache.shape) == tuple(k_cache.shape), "K/V cache shapes must match"
+    if blocks is None:
+        assert k_cache.shape[0] == batch, "K/V cache batch mismatch"
     assert page_indices.shape[0] == batch, "page_indices batch mismatch"
     assert page_indices.shape[1] == num_kv_heads, "page_indices must be keyed by KV heads"
     if k_cache.stride() != v_cache.stride():
@@ -216,10 +243,10 @@ def paged_entmax_decode(q, k_cache, v_cache, out, cache_seqlens, page_indices, p
     if q_seqlens is not None:
         qsl = q_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
     if kv_rows is None:
-        kv_rows = k_cache.shape[2]
+        kv_rows = k_cache.shape[2] if blocks is None else blocks.table.shape[1] * page_size
     call("ekv_paged_entmax_decode",
          q3.data_ptr(), q3.stride(0), q3.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
-         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), kv_rows,
+         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), kv_rows, *_bt_args(blocks),
          page_indices.data_ptr(), page_indices.stride(0), page_indices.stride(1), n_slots,
          cache_seqlens.data_ptr(), cache_seqlens.stride(0), cache_seqlens.stride(1),
          ptr(qsl), ptr(slopes), ptr(tau_in), tau.data_ptr(), tau_mode, iters,
@@ -238,6 +265,7 @@ def topk_paged_entmax_decode(q, k_min, k_max, scores, k_select: int, last_page: 
                              alibi_slopes=None, q_seqlens=None,
                              workspace: DecodeWorkspace | None = None, kv_rows: int | None = None,
                              taus_out: torch.Tensor | None = None,
+                             blocks: KVBlocks | None = None,
                              seq_lens: torch.Tensor | None = None):
     """Criticality + top-k + exact-tau decode of one step (ekv_topk_paged_entmax_decode).
 
@@ -284,12 +312,12 @@ def topk_paged_entmax_decode(q, k_min, k_max, scores, k_select: int, last_page: 
     if q_seqlens is not None:
         qsl = q_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
     if kv_rows is None:
-        kv_rows = k_cache.shape[2]
+        kv_rows = k_cache.shape[2] if blocks is None else blocks.table.shape[1] * page_size
     call("ekv_topk_paged_entmax_decode",
          q3.data_ptr(), q3.stride(0), q3.stride(1), k_min.data_ptr(), k_max.data_ptr(),
          k_min.stride(0), k_min.stride(1), k_min.stride(2), scores.data_ptr(), num_pages,
          seq_len, q_pos, k_select, last_page, k_cache.data_ptr(), v_cache.data_ptr(),
-         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), kv_rows,
+         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), kv_rows, *_bt_args(blocks),
          page_indices.data_ptr(), page_indices.stride(0), page_indices.stride(1),
          cache_seqlens.data_ptr(), cache_seqlens.stride(0), cache_seqlens.stride(1),
          ptr(qsl), ptr(slopes), ptr(seq_lens), tau.data_ptr(), niter, o_target.data_ptr(),
@@ -553,7 +581,8 @@ def gaussian_paged_entmax_decode(q, k_cache, v_cache, out, buffers: GaussianBuff
                                  iters: int, workspace: DecodeWorkspace, alibi_slopes=None,
                                  q_seqlens=None, kv_rows=None, eps: float = 1e-4,
                                  tau_iters: int = 120, tol: float = 1e-6,
-                                 seq_lens: torch.Tensor | None = None):
+                                 seq_lens: torch.Tensor | None = None,
+                                 blocks: KVBlocks | None = None):
     """Selection + decode of one Gaussian-aware step after compute_page_gaussian_moments
     (ekv_gaussian_paged_entmax_decode): global moments and tau-hat (unless
     ``tau_hat_given``), threshold select + pack + clamp (``tau_clamped`` None =
@@ -579,7 +608,7 @@ def gaussian_paged_entmax_decode(q, k_cache, v_cache, out, buffers: GaussianBuff
     o_target = o3 if direct else torch.empty(B, H, D, device=q.device, dtype=q.dtype)
     qsl = None if q_seqlens is None else q_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
     if kv_rows is None:
-        kv_rows = k_cache.shape[2]
+        kv_rows = k_cache.shape[2] if blocks is None else blocks.table.shape[1] * page_size
     call("ekv_gaussian_paged_entmax_decode",
          buffers.ws.data_ptr(), buffers.ws.numel(), buffers.mu_p.data_ptr(),
          buffers.sigma_p.data_ptr(), pages_for_stats, num_pages, buffers.mu_g.data_ptr(),
@@ -591,7 +620,8 @@ def gaussian_paged_entmax_decode(q, k_cache, v_cache, out, buffers: GaussianBuff
          counts.data_ptr(), tau_floor.data_ptr(), cache_seqlens.data_ptr(), int(last_page_size),
          ptr(tau_clamped), page_quantile_z(clamp_quantile, page_size), float(eps), ptr(effective),
          q3.data_ptr(), q3.stride(0), q3.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
-         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), kv_rows, ptr(qsl),
+         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), kv_rows, *_bt_args(blocks),
+         ptr(qsl),
          ptr(_alibi_f32(alibi_slopes, q.device)), ptr(seq_lens), tau_out.data_ptr(),
          int(tau_mode), int(iters),
          o_target.data_ptr(), o_target.stride(0), o_target.stride(1), float(alpha),

@@ -20,10 +20,19 @@ constructor, methods and attributes.  What changes is the storage:
   length.  ``seq_lens`` (device int32 [B]) then drives every kernel: each
   sequence has its own pages, last page, statistics and append position;
   ``seq_len`` is the longest length and fixes the buffer shapes.
+* Block pool (no counterpart in the reference either): with
+  ``block_pool=True`` K and V live in a pool ``[num_blocks, Hkv, page_size,
+  D]`` shared by the batch, and a block table (device int32 [B, pages])
+  maps page p of sequence b to its block.  Blocks are handed out from a free
+  list as pages fill (page-major over the batch, so the sequences' blocks
+  interleave in the pool), the statistics stay per sequence, and every kernel
+  reads K/V through the table.  ``k_cache``/``v_cache`` then gather a
+  contiguous copy.
 """
 
 from __future__ import annotations
 
+from collections import deque
 from typing import Optional
 
 import torch
@@ -39,10 +48,17 @@ class PagedKVCache:
     """KV cache with paged min/max/mean/std metadata (kv_cache.py:16-38)."""
 
     def __init__(self, page_size: int = 16, capacity: Optional[int] = None,
-                 headroom: int = 1024):
+                 headroom: int = 1024, block_pool: bool = False,
+                 num_blocks: Optional[int] = None):
         self.page_size = page_size
         self.capacity = capacity
         self.headroom = headroom
+        self.block_pool = block_pool
+        self.num_blocks = num_blocks  # pool size (default: every sequence's capacity)
+        self._table = None  # device int32 [B, pages cap] (block pool)
+        self._table_host = None
+        self._free = None
+        self._batch = 0
         self.seq_len = 0
         self.seq_lens: Optional[torch.Tensor] = None  # [B] int32 on the device (ragged batch)
         self._lens_host = None
@@ -68,13 +84,42 @@ class PagedKVCache:
     def num_pages(self) -> int:
         return (self.seq_len + self.page_size - 1) // self.page_size
 
+    def _gather_pool(self, pool):
+        """Contiguous [B, Hkv, seq_len, D] copy of a block pool's rows."""
+        P = self.num_pages
+        blocks = self._table[:, :P].long().clamp(min=0)  # unassigned pages read block 0
+        g = pool[blocks]  # [B, P, Hkv, ps, D]
+        B, _, Hkv, ps, D = g.shape
+        return g.permute(0, 2, 1, 3, 4).reshape(B, Hkv, P * ps, D)[:, :, : self.seq_len]
+
     @property
     def k_cache(self):
-        return None if self._k is None else self._k[:, :, : self.seq_len]
+        if self._k is None:
+            return None
+        return self._gather_pool(self._k) if self.block_pool else self._k[:, :, : self.seq_len]
 
     @property
     def v_cache(self):
-        return None if self._v is None else self._v[:, :, : self.seq_len]
+        if self._v is None:
+            return None
+        return self._gather_pool(self._v) if self.block_pool else self._v[:, :, : self.seq_len]
+
+    @property
+    def num_kv_heads(self) -> int:
+        return self._k.shape[1]
+
+    @property
+    def block_table(self) -> Optional[torch.Tensor]:
+        """Device int32 [B, pages cap] (block pool only; -1 = no block yet)."""
+        return self._table
+
+    def kv_operands(self):
+        """(k, v, kv_rows, blocks) as the decode launchers take them: the
+        capacity buffers [B, Hkv, cap, D], or the pool with its table."""
+        if self.block_pool:
+            return (self._k, self._v, self._table.shape[1] * self.page_size,
+                    K.KVBlocks(self._table, self._k.shape[0]))
+        return self._k, self._v, self._k.shape[2], None
 
     def _stat(self, buf, j):
         return None if buf is None else buf[:, :, : self.num_pages, j]
@@ -105,14 +150,16 @@ class PagedKVCache:
         reference's caller passes as ``cache_seqlens``, tests/test_topk.py:81-85)."""
         ps = self.page_size
         lens = self.seq_lens if self.seq_lens is not None else torch.full(
-            (self._k.shape[0],), self.seq_len, dtype=torch.int32, device=self._k.device)
+            (self._batch,), self.seq_len, dtype=torch.int32, device=self._k.device)
         pages = (lens + ps - 1) // ps
         k = torch.clamp(pages - 1, min=0, max=token_budget // ps)
         return (k * ps + lens - (pages - 1) * ps).to(torch.int32)
 
     @property
     def kv_capacity(self) -> int:
-        return 0 if self._k is None else self._k.shape[2]
+        if self._k is None:
+            return 0
+        return self._table.shape[1] * self.page_size if self.block_pool else self._k.shape[2]
 
     # ------------------------------------------------------------- storage
     def _allocate(self, batch, num_heads, cap, head_dim, dtype, device):
@@ -125,6 +172,10 @@ class PagedKVCache:
         return k, v, bounds, moments
 
     def _grow(self, needed: int):
+        if self.block_pool:
+            self._grow_table(_round_up(max(needed, 2 * self.kv_capacity), self.page_size)
+                             // self.page_size)
+            return
         B, H, cap, D = self._k.shape
         new_cap = max(needed, 2 * cap)
         k, v, bounds, moments = self._allocate(B, H, new_cap, D, self._k.dtype, self._k.device)
@@ -134,6 +185,87 @@ class PagedKVCache:
         bounds[:, :, :pc].copy_(self._bounds)
         moments[:, :, :pc].copy_(self._moments)
         self._k, self._v, self._bounds, self._moments = k, v, bounds, moments
+
+    # ------------------------------------------------------------- block pool
+    def _grow_table(self, pcap: int):
+        """Widen the block table (and the statistics) to ``pcap`` pages."""
+        B, old = self._table_host.shape
+        table = torch.full((B, pcap), -1, dtype=torch.int32)
+        table[:, :old] = self._table_host
+        self._table_host = table
+        self._table = table.to(self._k.device)
+        H, D = self._bounds.shape[1], self._bounds.shape[4]
+        bounds = torch.zeros(B, H, pcap, 2, D, dtype=self._k.dtype, device=self._k.device)
+        moments = torch.zeros_like(bounds)
+        bounds[:, :, :old].copy_(self._bounds)
+        moments[:, :, :old].copy_(self._moments)
+        self._bounds, self._moments = bounds, moments
+
+    def _take_block(self) -> int:
+        if not self._free:
+            # pool exhausted: double it (block ids stay valid)
+            n = self._k.shape[0]
+            k = torch.empty((2 * n,) + tuple(self._k.shape[1:]), dtype=self._k.dtype,
+                            device=self._k.device)
+            v = torch.empty_like(k)
+            k[:n].copy_(self._k)
+            v[:n].copy_(self._v)
+            self._k, self._v = k, v
+            self._free.extend(range(n, 2 * n))
+        return self._free.popleft()
+
+    def _init_pool(self, k, v, seq_len, cap):
+        B, H, _, D = k.shape
+        ps = self.page_size
+        pcap = _round_up(max(cap, ps), ps) // ps
+        nblocks = self.num_blocks if self.num_blocks is not None else B * pcap
+        P = (seq_len + ps - 1) // ps
+        lens = self._lens_host if self._lens_host is not None else torch.full((B,), seq_len)
+        pages = (lens + ps - 1) // ps
+        if int(pages.sum()) > nblocks:
+            raise ValueError(f"num_blocks={nblocks} cannot hold {int(pages.sum())} pages")
+        self._k = torch.empty(nblocks, H, ps, D, dtype=k.dtype, device=k.device)
+        self._v = torch.empty_like(self._k)
+        self._bounds = torch.zeros(B, H, pcap, 2, D, dtype=k.dtype, device=k.device)
+        self._moments = torch.zeros_like(self._bounds)
+        self._free = deque(range(nblocks))
+        table = torch.full((B, pcap), -1, dtype=torch.int32)
+        for p in range(P):  # page-major: the sequences' blocks interleave
+            for b in range(B):
+                if p < int(pages[b]):
+                    table[b, p] = self._free.popleft()
+        self._table_host = table
+        self._table = table.to(k.device)
+        if P == 0:
+            return None
+        # page-padded contiguous copy: the statistics source and the scatter source
+        kp = torch.zeros(B, H, P * ps, D, dtype=k.dtype, device=k.device)
+        vp = torch.zeros_like(kp)
+        kp[:, :, :seq_len].copy_(k[:, :, :seq_len])
+        vp[:, :, :seq_len].copy_(v[:, :, :seq_len])
+        valid = table[:, :P] >= 0
+        idx = table[:, :P][valid].long().to(k.device)
+        vd = valid.to(k.device)
+        self._k.index_copy_(0, idx, kp.view(B, H, P, ps, D).permute(0, 2, 1, 3, 4)[vd])
+        self._v.index_copy_(0, idx, vp.view(B, H, P, ps, D).permute(0, 2, 1, 3, 4)[vd])
+        return kp
+
+    def _assign_append_blocks(self, pos: int):
+        """Give every sequence whose next row opens a page a block for it."""
+        ps = self.page_size
+        lens = self._lens_host if self._lens_host is not None else torch.full(
+            (self._batch,), pos, dtype=torch.int64)
+        need = int(lens.max()) // ps + 1
+        if need > self._table_host.shape[1]:
+            self._grow_table(max(need, 2 * self._table_host.shape[1]))
+        changed = False
+        for b in range(self._batch):
+            page = int(lens[b]) // ps
+            if self._table_host[b, page] < 0:
+                self._table_host[b, page] = self._take_block()
+                changed = True
+        if changed:
+            self._table.copy_(self._table_host)
 
     def initialize(self, k: torch.Tensor, v: torch.Tensor, seq_lens=None):
         """Initialize the cache with prefill keys/values (kv_cache.py:40-70).
@@ -147,7 +279,7 @@ class PagedKVCache:
         self.seq_lens = None
         self._lens_host = None
         if seq_lens is not None:
-            host = torch.as_tensor(seq_lens, dtype=torch.int64).reshape(-1).cpu()
+            host = torch.as_tensor(seq_lens, dtype=torch.int64).reshape(-1).cpu().clone()
             if host.numel() != batch:
                 raise ValueError(f"seq_lens has {host.numel()} entries for a batch of {batch}")
             if bool((host < 1).any()) or bool((host > seq_len).any()):
@@ -157,15 +289,20 @@ class PagedKVCache:
             seq_len = int(host.max())
         cap = self.capacity if self.capacity is not None else seq_len + self.headroom
         cap = max(cap, seq_len + 1)
-        self._k, self._v, self._bounds, self._moments = self._allocate(
-            batch, num_heads, cap, head_dim, k.dtype, k.device)
-        self._k[:, :, :seq_len].copy_(k[:, :, :seq_len])
-        self._v[:, :, :seq_len].copy_(v[:, :, :seq_len])
+        self._batch = batch
+        if self.block_pool:
+            src = self._init_pool(k, v, seq_len, cap)
+        else:
+            self._k, self._v, self._bounds, self._moments = self._allocate(
+                batch, num_heads, cap, head_dim, k.dtype, k.device)
+            self._k[:, :, :seq_len].copy_(k[:, :, :seq_len])
+            self._v[:, :, :seq_len].copy_(v[:, :, :seq_len])
+            src = self._k
         self.seq_len = seq_len
         self._page_indices_buf = None
         self._page_indices_last_page = None
         if seq_len > 0:
-            K.page_stats(self._k, self._bounds[:, :, :, 0], self._bounds[:, :, :, 1],
+            K.page_stats(src, self._bounds[:, :, :, 0], self._bounds[:, :, :, 1],
                          self._moments[:, :, :, 0], self._moments[:, :, :, 1], seq_len,
                          self.page_size, 0, self.num_pages, seq_lens=self.seq_lens)
 
@@ -179,12 +316,16 @@ class PagedKVCache:
                 self.append(k_new[:, :, t:t + 1], v_new[:, :, t:t + 1])
             return
         pos = self.seq_len
-        if pos + 1 > self.kv_capacity:
+        blocks = None
+        if self.block_pool:
+            self._assign_append_blocks(pos)
+            blocks = K.KVBlocks(self._table, self._k.shape[0])
+        elif pos + 1 > self.kv_capacity:
             self._grow(pos + 1 + self.headroom)
         K.append_token(k_new[:, :, 0], v_new[:, :, 0], self._k, self._v,
                        self._bounds[:, :, :, 0], self._bounds[:, :, :, 1],
                        self._moments[:, :, :, 0], self._moments[:, :, :, 1], pos, self.page_size,
-                       pos_per_batch=self.seq_lens)
+                       pos_per_batch=self.seq_lens, blocks=blocks)
         if self.seq_lens is not None:
             # every sequence grows by one token at its own position
             self.seq_lens.add_(1)

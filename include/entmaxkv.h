@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define EKV_ABI_VERSION 3
+#define EKV_ABI_VERSION 4
 
 const char* ekv_last_error(void);
 int ekv_abi_version(void);
@@ -51,13 +51,17 @@ int ekv_page_stats(const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_
 
 /* In-place append of one token per (b, kv head) at row `pos` (or
  * pos_per_batch[b] when non-null, negative = skip) and recompute of that
- * page's statistics.  K and V share strides.  Replaces the torch.cat append
+ * page's statistics.  K and V share strides.  With block_table non-null
+ * (see ekv_paged_entmax_decode) the row goes to block
+ * block_table[b][pos / page_size] of the pool (skipped when the id lies
+ * outside [0, bt_blocks)).  Replaces the torch.cat append
  * and last-page recompute of PagedKVCache.append, kv_cache.py:72-116. */
 int ekv_append(const void* k_new, const void* v_new, int64_t new_stride_b, int64_t new_stride_h,
                void* k, void* v, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_row,
                void* kmin, void* kmax, void* kmean, void* kstd, int64_t s_stride_b,
                int64_t s_stride_h, int64_t s_stride_page, int B, int Hkv, int D, int pos,
-               const int32_t* pos_per_batch, int page_size, int dtype, void* stream);
+               const int32_t* pos_per_batch, const int32_t* block_table, int64_t bt_stride_b,
+               int bt_blocks, int page_size, int dtype, void* stream);
 
 /* Page criticality scores [B, H, num_pages] (query dtype, contiguous):
  * sum_d max(q_d kmin_pd, q_d kmax_pd) (+ ALiBi bonus when alibi_slopes [H] is
@@ -90,11 +94,22 @@ int64_t ekv_decode_workspace_bytes(int B, int H, int Hkv, int D, int splits, int
  *   Halley/Newton corrections, final tau written to tau (may alias tau_in).
  * qscale = (alpha-1)/sqrt(D) rounded to the storage dtype.  kv_rows bounds
  * the rows addressable per (b, kv head); out-of-range page ids are skipped.
+ * K/V addressing: with block_table null, row r of (b, kv head) is at
+ * b * kv_stride_b + kv_head * kv_stride_h + r * kv_stride_row (the
+ * reference's contiguous cache); with a block table [B, >= kv_rows /
+ * page_size] int32 (row stride bt_stride_b) over a pool of bt_blocks blocks,
+ * it is at blk * kv_stride_b + kv_head * kv_stride_h + (r % page_size) *
+ * kv_stride_row with blk = block_table[b][r / page_size] (e.g. a pool
+ * [bt_blocks, Hkv, page_size, D]); block ids outside [0, bt_blocks) are
+ * skipped.  The block table has no counterpart in the reference, whose cache
+ * is contiguous (kv_cache.py:81-82).  kv_stride_b and kv_stride_h must be
+ * multiples of kv_stride_row.
  * Replaces kernels/adadecode_paged.py:567-762 and
  * kernels/adadecode_paged_gaussian_tau.py:192-331. */
 int ekv_paged_entmax_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k,
                             const void* v, int64_t kv_stride_b, int64_t kv_stride_h,
-                            int64_t kv_stride_row, int64_t kv_rows, const int32_t* page_indices,
+                            int64_t kv_stride_row, int64_t kv_rows, const int32_t* block_table,
+                            int64_t bt_stride_b, int bt_blocks, const int32_t* page_indices,
                             int64_t pi_stride_b, int64_t pi_stride_h, int n_slots,
                             const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
                             const int32_t* q_seqlens, const float* alibi_slopes,
@@ -117,6 +132,7 @@ int ekv_topk_paged_entmax_decode(
     int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, void* scores, int num_pages,
     int seq_len, int q_pos, int k_select, int last_page, const void* k, const void* v,
     int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+    const int32_t* block_table, int64_t bt_stride_b, int bt_blocks,
     int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h,
     const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
     const int32_t* q_seqlens, const float* alibi_slopes, const int32_t* seq_lens, float* tau,
@@ -142,6 +158,7 @@ int ekv_topk_paged_entmax_decode_noalloc(
     int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, void* scores, int num_pages,
     int seq_len, int q_pos, int k_select, int last_page, const void* k, const void* v,
     int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+    const int32_t* block_table, int64_t bt_stride_b, int bt_blocks,
     int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h,
     const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
     const int32_t* q_seqlens, const float* alibi_slopes, const int32_t* seq_lens, float* tau,
@@ -240,7 +257,8 @@ int ekv_gaussian_paged_entmax_decode(
     float* tau_floor, int32_t* cache_seqlens, int last_page_size, float* tau_clamped,
     float z_clamp, float eps, float* effective_margins, const void* q, int64_t q_stride_b,
     int64_t q_stride_h, const void* k, const void* v, int64_t kv_stride_b, int64_t kv_stride_h,
-    int64_t kv_stride_row, int64_t kv_rows, const int32_t* q_seqlens, const float* alibi_slopes,
+    int64_t kv_stride_row, int64_t kv_rows, const int32_t* block_table, int64_t bt_stride_b,
+    int bt_blocks, const int32_t* q_seqlens, const float* alibi_slopes,
     const int32_t* seq_lens, float* tau, int tau_mode, int iters, void* out,
     int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale, int page_size, int B,
     int H, int Hkv, int D, int max_tokens, void* workspace, int64_t workspace_bytes, int dtype,

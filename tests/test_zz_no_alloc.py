@@ -56,7 +56,7 @@ def _run(c, noalloc):
     args = [q3.data_ptr(), q3.stride(0), q3.stride(1), kmin.data_ptr(), kmax.data_ptr(),
             kmin.stride(0), kmin.stride(1), kmin.stride(2), scores.data_ptr(), P - 1, c["S"],
             c["S"] - 1, k, P - 1, kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1),
-            kc.stride(2), kc.shape[2], pidx.data_ptr(), pidx.stride(0), pidx.stride(1),
+            kc.stride(2), kc.shape[2], None, 0, 0, pidx.data_ptr(), pidx.stride(0), pidx.stride(1),
             seqlens.data_ptr(), seqlens.stride(0), seqlens.stride(1), None, None, None,
             tau.data_ptr(), 2, out.data_ptr(), out.stride(0), out.stride(1), 1.5,
             qscale_for(1.5, D, dt), ps, B, H, Hkv, D, splits, max_tokens]
@@ -98,7 +98,8 @@ def test_noalloc_rejects_a_step_beyond_the_scratch():
     # every pointer null: were the size check to pass, the null-pointer check
     # behind it would still refuse the call, so nothing can launch
     args = [None, 0, 0, None, None, 0, 0, 0, None, 4096, 4096 * ps, 4096 * ps - 1, 127, 4095,
-            None, None, 0, 0, 0, 4096 * ps, None, 0, 0, None, 0, 0, None, None, None, None, 2,
+            None, None, 0, 0, 0, 4096 * ps, None, 0, 0, None, 0, 0, None, 0, 0, None, None,
+            None, None, 2,
             None, 0, 0, 1.5, 0.0442, ps, B, H, Hkv, D, 16, max_tokens, 1,
             ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)]
     with pytest.raises(ValueError, match="static scratch"):
