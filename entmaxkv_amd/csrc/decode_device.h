@@ -35,6 +35,13 @@ __device__ unsigned long long ekv_wave_timers[256 * 16 * 8];
   ekv_wave_timers[(blockIdx.x * 16 + (threadIdx.x >> 6)) * 8 + (i)] = wall_clock64()
 #define EKV_STAMP(i) \
   if (threadIdx.x == 0 && blockIdx.x < 4096) ekv_phase_timers[blockIdx.x * 16 + (i)] = wall_clock64()
+#ifdef EKV_SEL_STAMPS
+#define EKV_TSTAMP(i)
+#define EKV_SSTAMP(i) EKV_STAMP(i)
+#else
+#define EKV_TSTAMP(i) EKV_STAMP(i)
+#define EKV_SSTAMP(i)
+#endif
 // slot 6 in the top-k launch: the top-k threshold found (topk_device.h stamp
 // 3); slots 12-15: the group select's stages (stamps 12-15)
 #define EKV_CSTAMP(i)  \
@@ -48,6 +55,8 @@ __device__ unsigned long long ekv_wave_timers[256 * 16 * 8];
 #else
 #define EKV_STAMP(i)
 #define EKV_WSTAMP(i)
+#define EKV_TSTAMP(i)
+#define EKV_SSTAMP(i)
 #endif
 
 #include "ekv_common.h"
@@ -743,7 +752,7 @@ __device__ __forceinline__ float solve_tau(S& sp, const DecodeArgs& a, const flo
       }
     }
     const float gmax = pre_max ? m : sp.max(m);
-    EKV_STAMP(7);
+    EKV_TSTAMP(7);
     const float t0 = gmax - 1.0f;
     for (int b0 = 0; b0 < n; b0 += S::kStride * kBatch) {
 #pragma unroll
@@ -756,18 +765,18 @@ __device__ __forceinline__ float solve_tau(S& sp, const DecodeArgs& a, const flo
       }
     }
     sp.sync();
-    EKV_STAMP(8);
+    EKV_TSTAMP(8);
     float t_lo, t_hi;
     if ((alpha == 2.0f || alpha == 1.5f) && n <= kExactInitTokens)
       histogram_init_wave(hist[kBins - 1 - min(sp.lane, kBins - 1)], gmax, alpha, t, t_lo, t_hi);
     else
       histogram_init(hist, gmax, alpha, t, t_lo, t_hi);
-    EKV_STAMP(9);
+    EKV_TSTAMP(9);
     for (int it = 0; it < a.iters; ++it) {
       float a0, a1, a2;
       accumulate_pass(sp, sc, n, t, alpha, c0, a0, a1, a2);
       halley_bisect(t, t_lo, t_hi, a0, a1, a2, c0, c1);
-      if (it < 2) EKV_STAMP(10 + it);
+      if (it < 2) EKV_TSTAMP(10 + it);
     }
   } else {
     t = tau_in;
@@ -1156,9 +1165,36 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
         a.slopes, (T*)t.scores, a.H, t.num_pages, r.count, a.page_size, r.seq_len, r.q_pos, b,
         kvh, G == 1 ? (keep ? keys : nullptr) : head_keys,
         G == 1 && keep ? &sel_hist[0][0] : nullptr);
+  } else if (G > 1 && head_keys &&
+             (t.num_pages * (int)sizeof(T)) % 16 == 0 && ((uintptr_t)sbase & 15) == 0) {
+    // every query head's keys into LDS once (the select reads them per pass):
+    // 16-byte loads (each head's row of scores is 16-byte aligned, and the
+    // last vector of a row stays within it), four per thread in flight
+    constexpr int E = 16 / sizeof(T);
+    const int per_row = (r.count + E - 1) / E;
+    const int total = G * per_row;
+    for (int i0 = 0; i0 < total; i0 += 4 * kHeadThreads) {
+      uint4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = min(i0 + j * kHeadThreads + (int)threadIdx.x, total - 1);
+        v[j] = ld16(sbase + (int64_t)(i / per_row) * t.num_pages + (i % per_row) * E);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = i0 + j * kHeadThreads + (int)threadIdx.x;
+        if (i < total) {
+          const int g = i / per_row, p0 = (i % per_row) * E;
+          T x[E];
+          __builtin_memcpy(x, &v[j], 16);
+#pragma unroll
+          for (int e = 0; e < E; ++e)
+            if (p0 + e < r.count) head_keys[g * t.num_pages + p0 + e] = topk::ScoreKey<T>::key(x[e]);
+        }
+      }
+    }
   } else if (G > 1 && head_keys) {
-    // every query head's keys into LDS once (the select reads them per pass);
-    // eight loads per thread in flight before their stores
+    // unaligned rows: element loads, eight per thread in flight
     const int total = G * r.count;
     for (int i0 = 0; i0 < total; i0 += 8 * kHeadThreads) {
       T sv[8];
@@ -1342,8 +1378,11 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
                                : sel.last_page_size;
   int n = count > 0 ? (count - 1) * sel.page_size + lps : 0;
   n = min(n, min(count * sel.page_size, a.max_tokens));
-  // the first kTablePages page ids are already in s_pages
-  if (n <= a.stage_cap) {
+  // the first kTablePages page ids are already in s_pages (all of them when
+  // count <= kTablePages: the decode then reads no page id from global memory)
+  if (n <= a.stage_cap && count <= kTablePages) {
+    decode_head_body<T, LPR, G, UD, true, true>(a, b, kvh, n, stage, a.stage_cap, sh);
+  } else if (n <= a.stage_cap) {
     decode_head_body<T, LPR, G, UD, true>(a, b, kvh, n, stage, a.stage_cap, sh, true);
   } else {
     float* ws = a.ws_scores + ((int64_t)b * a.H + kvh * G) * a.max_tokens;

@@ -29,7 +29,9 @@ using namespace ekv::gauss;
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kMomentUnroll = 2;
+// pages per row segment per round (two rounds in flight): one measured
+// slightly faster than two and four at the headline shape
+constexpr int kMomentUnroll = 1;
 
 template <typename T, int LPR, int G>
 __global__ __launch_bounds__(moment_threads(G)) void moments_kernel(MomentsArgs a) {

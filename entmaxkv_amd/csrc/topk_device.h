@@ -12,6 +12,9 @@
 #ifndef EKV_WSTAMP
 #define EKV_WSTAMP(i)
 #endif
+#ifndef EKV_SSTAMP
+#define EKV_SSTAMP(i)
+#endif
 
 namespace ekv {
 namespace topk {
@@ -298,6 +301,7 @@ __device__ __forceinline__ void radix_threshold_group(KeyOf key_of, int n, int k
         }
       }
     }
+    EKV_SSTAMP(7 + 2 * pass);
     __syncthreads();
     const int top = 255 - 4 * lane;
 #pragma unroll
@@ -330,6 +334,7 @@ __device__ __forceinline__ void radix_threshold_group(KeyOf key_of, int n, int k
       prefix[g] |= ((uint32_t)bin) << shift;
       kk[g] = rem;
     }
+    EKV_SSTAMP(8 + 2 * pass);
     pmask |= 255u << shift;
   }
 #pragma unroll
