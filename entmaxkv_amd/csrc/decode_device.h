@@ -369,10 +369,12 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
   // Rows of compacted tokens c0 + u * SEGS + seg and their K loads.  The loads
   // are unconditional (an invalid token re-reads row 0 and is masked), so
   // all U of them are in flight together.
-  auto fetch = [&](int c0, int (&rows)[U], uint4 (&kv)[U]) {
-    int64_t off[U];
+  // (generic over the buffer length N: U rows, or 1 for the folded remainder)
+  auto fetch = [&](int c0, auto& rows, auto& kv) {
+    constexpr int N = sizeof(kv) / sizeof(kv[0]);
+    int64_t off[N];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < N; ++u) {
       const int c = c0 + u * SEGS + seg;
       rows[u] = kNoRow;
       off[u] = 0;  // an invalid token re-reads the cache's first element
@@ -387,11 +389,12 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) kv[u] = ld16(kbase + off[u] + col);
+    for (int u = 0; u < N; ++u) kv[u] = ld16(kbase + off[u] + col);
   };
-  auto consume = [&](int c0, const int (&rows)[U], const uint4 (&kv)[U]) {
+  auto consume = [&](int c0, const auto& rows, const auto& kv) {
+    constexpr int N = sizeof(kv) / sizeof(kv[0]);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < N; ++u) {
       const int c = c0 + u * SEGS + seg;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -412,10 +415,18 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
   // loads unconditionally, so the compiler's wait counts keep the other
   // buffer's loads in flight during each consume; the last one or two rounds
   // are peeled.
-  int rows_a[U], rows_b[U];
-  uint4 kv_a[U], kv_b[U];
-  const int rounds = c_end > c_begin ? (c_end - c_begin + ROWS - 1) / ROWS : 0;
+  // A remainder of at most one row per segment after the full rounds is
+  // folded into the first round (loaded with it, scored at the end) instead
+  // of costing a round trip of its own: k pages plus a one-token last page
+  // (the top-k step after an append) is 2 full rounds and one row.
+  int rows_a[U], rows_b[U], rows_x[1];
+  uint4 kv_a[U], kv_b[U], kv_x[1];
+  const int nrows = c_end > c_begin ? c_end - c_begin : 0;
+  const int full = nrows / ROWS, rem = nrows - full * ROWS;
+  const bool fold = full > 0 && rem > 0 && rem <= SEGS;
+  const int rounds = fold ? full : (nrows + ROWS - 1) / ROWS;
   if (rounds > 0) fetch(c_begin, rows_a, kv_a);
+  if (fold) fetch(c_begin + full * ROWS, rows_x, kv_x);
   int r = 0;
   for (; r + 2 < rounds; r += 2) {
     fetch(c_begin + (r + 1) * ROWS, rows_b, kv_b);
@@ -430,6 +441,7 @@ __device__ __forceinline__ void score_rows(const DecodeArgs& a, int b, int kvh, 
   } else if (r < rounds) {
     consume(c_begin + r * ROWS, rows_a, kv_a);
   }
+  if (fold) consume(c_begin + full * ROWS, rows_x, kv_x);
   if (kpos && sl == 0) {
     // explicit key positions: the ALiBi term (and the running max) over the
     // scores this lane wrote above (lane 0 of each row segment: it alone
