@@ -1158,11 +1158,14 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
   const int bkv = blockIdx.x;
   const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
   uint32_t* keys = reinterpret_cast<uint32_t*>(stage);
+  // the scan's chunk counter (and, G == 1, the select's histograms) start at zero
+  __shared__ int scan_next;
+  if (threadIdx.x == 0) scan_next = 0;
   if (G == 1) {
     for (int i = threadIdx.x; i < (int)(sizeof(sel_hist) / 4); i += kHeadThreads)
       (&sel_hist[0][0])[i] = 0u;
-    __syncthreads();
   }
+  __syncthreads();
   const topk::Ragged r = topk::ragged_topk(t.seq_lens, b, a.page_size, t.num_pages, t.seq_len,
                                            t.q_pos, t.k, t.last_page);
   const bool keep = r.count <= t.key_cap;
@@ -1176,7 +1179,7 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
         (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
         a.slopes, (T*)t.scores, a.H, t.num_pages, r.count, a.page_size, r.seq_len, r.q_pos, b,
         kvh, G == 1 ? (keep ? keys : nullptr) : head_keys,
-        G == 1 && keep ? &sel_hist[0][0] : nullptr);
+        G == 1 && keep ? &sel_hist[0][0] : nullptr, &scan_next);
   } else if (G > 1 && head_keys &&
              (t.num_pages * (int)sizeof(T)) % 16 == 0 && ((uintptr_t)sbase & 15) == 0) {
     // every query head's keys into LDS once (the select reads them per pass):

@@ -794,7 +794,7 @@ __device__ __forceinline__ T* criticality_scan_head(
     const T* __restrict__ kmax, int64_t ssb, int64_t ssh, int64_t ssp,
     const float* __restrict__ slopes, T* __restrict__ scores, int H, int stride, int num_pages,
     int page_size, int seq_len, int q_pos, int b, int kvh, uint32_t* lds_keys,
-    unsigned* hist0 = nullptr) {
+    unsigned* hist0 = nullptr, int* lds_next = nullptr) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int SEGS = NT / LPR;
   constexpr int ROUND = SEGS * U;
@@ -818,11 +818,12 @@ __device__ __forceinline__ T* criticality_scan_head(
   const T* kmx = kmax + b * ssb + kvh * ssh;
   T* sbase = scores + ((int64_t)b * H + h0) * stride;
 
-  for (int p0 = 0; p0 < num_pages; p0 += ROUND) {
+  // pages base + u * step + off for u < U
+  auto body = [&](int base, int step, int off) {
     uint4 lo[U], hi[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int p = p0 + u * SEGS + seg;
+      const int p = base + u * step + off;
       if (p < num_pages) {
         lo[u] = ld16(kmn + (int64_t)p * ssp + col);
         hi[u] = ld16(kmx + (int64_t)p * ssp + col);
@@ -830,7 +831,7 @@ __device__ __forceinline__ T* criticality_scan_head(
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int p = p0 + u * SEGS + seg;
+      const int p = base + u * step + off;
       uint32_t key = 0;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -852,6 +853,28 @@ __device__ __forceinline__ T* criticality_scan_head(
         if (hist0) atomicAdd(&hist0[key >> (ScoreKey<T>::kBits - 8)], 1u);
       }
     }
+  };
+  if (lds_next) {
+    // waves take chunks of U * (64 / LPR) consecutive pages from a shared
+    // counter (zero and visible on entry), the next chunk's index fetched
+    // while the current chunk's loads are in flight: a wave slowed by its
+    // memory accesses takes fewer chunks, so the waves finish together
+    constexpr int WSEG = 64 / LPR;
+    constexpr int CHUNK = WSEG * U;
+    const int lane = threadIdx.x & 63;
+    auto grab = [&]() {
+      int v = 0;
+      if (lane == 0) v = atomicAdd(lds_next, 1);
+      return __builtin_amdgcn_readfirstlane(v);
+    };
+    int c = grab();
+    while (c * CHUNK < num_pages) {
+      const int c_next = grab();
+      body(c * CHUNK, WSEG, seg % WSEG);
+      c = c_next;
+    }
+  } else {
+    for (int p0 = 0; p0 < num_pages; p0 += ROUND) body(p0, SEGS, seg);
   }
   EKV_WSTAMP(0);
   return sbase;
