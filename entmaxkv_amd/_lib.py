@@ -43,6 +43,11 @@ SIGNATURES = {
                                          I64, I64, I64, I64, P, I64, I, P, I64, I64, P, I64, I64,
                                          P, P, P, P, I, P, I64, I64, F, F, I, I, I, I, I, I, I, P,
                                          I64, I, P]),
+    "ekv_append_topk_paged_entmax_decode": (I, [P, P, I64, I64, P, P, I,
+                                                P, I64, I64, P, P, I64, I64, I64, P, I, I, I, I,
+                                                I, P, P, I64, I64, I64, I64, P, I64, I, P, I64,
+                                                I64, P, I64, I64, P, P, P, P, I, P, I64, I64, F,
+                                                F, I, I, I, I, I, I, I, P, I64, I, P]),
     "ekv_topk_paged_entmax_decode_noalloc": (I, [P, I64, I64, P, P, I64, I64, I64, P, I, I, I, I,
                                                  I, P, P, I64, I64, I64, I64, P, I64, I, P, I64,
                                                  I64, P, I64, I64, P, P, P, P, I, P, I64, I64, F,
@@ -70,7 +75,7 @@ SIGNATURES = {
     "ekv_entmax_rows_backward": (I, [P, I64, P, I64, P, I64, I64, I, F, I, P]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib = None

@@ -42,8 +42,13 @@ def sparse_attention_decode_paged(
     batch, num_heads, _, head_dim = q.shape
     num_kv_heads = kv_cache.num_kv_heads
 
+    # a uniform batch's new row is written by the step's own launch
+    row = None
     if append_cache:
-        kv_cache.append(k_new, v_new)
+        if kv_cache.is_ragged or k_new.shape[2] != 1:
+            kv_cache.append(k_new, v_new)
+        else:
+            row = kv_cache.reserve_append(k_new, v_new)
 
     seq_len = kv_cache.seq_len
     page_size = kv_cache.page_size
@@ -61,6 +66,8 @@ def sparse_attention_decode_paged(
             max_tokens=(num_pages_to_select + 1) * page_size)
 
     if num_pages_to_select == 0:
+        if row is not None:
+            kv_cache.write_append(row)
         page_indices = kv_cache.select_topk(q, 0, alibi_slopes=alibi_slopes)
         kc, vc, rows, blocks = kv_cache.kv_operands()
         K.paged_entmax_decode(
@@ -79,5 +86,5 @@ def sparse_attention_decode_paged(
         q, kv_cache.k_min, kv_cache.k_max, scores, num_pages_to_select, last, kc,
         vc, out, page_indices, cache_seqlens, page_size, alpha, niter, seq_len,
         seq_len - 1, alibi_slopes=alibi_slopes, q_seqlens=q_seqlens, workspace=workspace,
-        kv_rows=rows, seq_lens=seq_lens, blocks=blocks)
+        kv_rows=rows, seq_lens=seq_lens, blocks=blocks, append=row)
     return out

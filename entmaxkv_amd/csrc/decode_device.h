@@ -62,6 +62,7 @@ __device__ unsigned long long ekv_wave_timers[256 * 16 * 8];
 #include "ekv_common.h"
 #include "topk_device.h"
 #include "gaussian_device.h"
+#include "append_device.h"
 
 namespace ekv {
 namespace dec {
@@ -1129,6 +1130,16 @@ struct SelectArgs {
   int head_keys;      // G > 1: every query head's page keys kept in LDS too
   int list_words;     // G > 1: LDS words of the candidate lists
   int prescored;      // the scores are already in `scores` (a split scan ran first)
+  // fused append (uniform batch): row app_pos of K and V from app_k / app_v
+  // [B, Hkv, D] rows (strides app_nsb, app_nsh) and the four statistics of
+  // its page (kmin, kmax above; app_kmean, app_kstd with the same strides),
+  // before anything reads them; app_k null: no append
+  const void* app_k = nullptr;
+  const void* app_v = nullptr;
+  int64_t app_nsb = 0, app_nsh = 0;
+  void* app_kmean = nullptr;
+  void* app_kstd = nullptr;
+  int app_pos = -1;
   const int32_t* seq_lens;  // [B] per-sequence lengths (ragged batch) or null
 };
 
@@ -1166,6 +1177,24 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
       (&sel_hist[0][0])[i] = 0u;
   }
   __syncthreads();
+  if (t.app_k && threadIdx.x < LPR) {
+    // the appended row and its page's statistics: the page is the last one,
+    // which the scan never reads; the K/V phases read the row after the
+    // select's barriers.  The first wave joins the scan afterwards (its
+    // chunks go to the others meanwhile).
+    const int pos = t.app_pos;
+    const int64_t o0 = kv_row_offset(a, b, kvh, (int64_t)(pos / a.page_size) * a.page_size);
+    if (o0 >= 0) {
+      const int64_t shift = o0 - (int64_t)(pos / a.page_size) * a.page_size * a.ksr;
+      const int64_t so = b * t.ssb + kvh * t.ssh + (int64_t)(pos / a.page_size) * t.ssp;
+      PageStatRows<T> rows{(T*)t.kmin + so, (T*)t.kmax + so, (T*)t.app_kmean + so,
+                           (T*)t.app_kstd + so};
+      append_row<T, LPR>((const T*)t.app_k + b * t.app_nsb + kvh * t.app_nsh,
+                         (const T*)t.app_v + b * t.app_nsb + kvh * t.app_nsh,
+                         (T*)a.k + shift, (T*)a.v + shift, a.ksr, pos, a.page_size, rows,
+                         (int)threadIdx.x * VEC);
+    }
+  }
   const topk::Ragged r = topk::ragged_topk(t.seq_lens, b, a.page_size, t.num_pages, t.seq_len,
                                            t.q_pos, t.k, t.last_page);
   const bool keep = r.count <= t.key_cap;

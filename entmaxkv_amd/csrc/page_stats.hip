@@ -11,6 +11,7 @@
 // HBM: each page's rows are read twice (min/max/sum, then the centred second
 // moment); the second read hits L2 because a workgroup owns whole pages.
 #include "ekv_common.h"
+#include "append_device.h"
 #include "../../include/entmaxkv.h"
 
 using namespace ekv;
@@ -130,70 +131,9 @@ __global__ __launch_bounds__(64) void append_kernel(
     kh = k + shift;
     vh = v + shift;
   }
-  Vec<T> kx, vx;
-  kx.load(kn + col);
-  vx.load(vn + col);
-  // raw 16-byte copies keep the stored bits identical to the inputs
-  *reinterpret_cast<uint4*>(kh + (int64_t)pos * ksr + col) = *reinterpret_cast<const uint4*>(kn + col);
-  *reinterpret_cast<uint4*>(vh + (int64_t)pos * ksr + col) = *reinterpret_cast<const uint4*>(vn + col);
-
-  const int page = pos / page_size;
-  const int r0 = page * page_size;
-  const int n_rows = pos - r0 + 1;
-  float mn[VEC], mx[VEC], sm[VEC];
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    mn[i] = kx.v[i];
-    mx[i] = kx.v[i];
-    sm[i] = 0.f;
-  }
-  for (int r = r0; r < pos; ++r) {
-    Vec<T> x;
-    x.load(kh + (int64_t)r * ksr + col);
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      mn[i] = fminf(mn[i], x.v[i]);
-      mx[i] = fmaxf(mx[i], x.v[i]);
-      sm[i] += x.v[i];
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) sm[i] += kx.v[i];
-  float mean[VEC], m2[VEC];
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    mean[i] = sm[i] / (float)n_rows;
-    m2[i] = 0.f;
-  }
-  for (int r = r0; r < pos; ++r) {
-    Vec<T> x;
-    x.load(kh + (int64_t)r * ksr + col);
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      float d = x.v[i] - mean[i];
-      m2[i] += d * d;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    float d = kx.v[i] - mean[i];
-    m2[i] += d * d;
-  }
-  const int64_t so = b * ssb + h * ssh + (int64_t)page * ssp;
-  Vec<T> o;
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) o.v[i] = mn[i];
-  o.store((T*)st.kmin + so + col);
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) o.v[i] = mx[i];
-  o.store((T*)st.kmax + so + col);
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) o.v[i] = mean[i];
-  o.store((T*)st.kmean + so + col);
-  const float inv_n = 1.0f / (float)n_rows;
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) o.v[i] = fmaxf(sqrtf(m2[i] * inv_n), 1e-6f);
-  o.store((T*)st.kstd + so + col);
+  const int64_t so = b * ssb + h * ssh + (int64_t)(pos / page_size) * ssp;
+  PageStatRows<T> rows{(T*)st.kmin + so, (T*)st.kmax + so, (T*)st.kmean + so, (T*)st.kstd + so};
+  append_row<T, LPR>(kn, vn, kh, vh, ksr, pos, page_size, rows, col);
 }
 
 template <typename T, int LPR>

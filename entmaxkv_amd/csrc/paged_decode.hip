@@ -176,7 +176,17 @@ extern "C" int ekv_paged_entmax_decode(
                       nullptr, 0, 0, KvBlocks{block_table, bt_stride_b, bt_blocks});
 }
 
-extern "C" int ekv_topk_paged_entmax_decode(
+// The appended row of ekv_append_topk_paged_entmax_decode (null: none).
+struct AppendSpec {
+  const void* k_new;
+  const void* v_new;
+  int64_t nsb, nsh;
+  void* kmean;
+  void* kstd;
+  int pos;
+};
+
+static int topk_step(
     const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kmin, const void* kmax,
     int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, void* scores, int num_pages,
     int seq_len, int q_pos, int k_select, int last_page, const void* k, const void* v,
@@ -187,7 +197,8 @@ extern "C" int ekv_topk_paged_entmax_decode(
     const int32_t* q_seqlens, const float* alibi_slopes, const int32_t* seq_lens, float* tau,
     int niter, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale,
     int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens, void* workspace,
-    int64_t workspace_bytes, int dtype, void* stream) {
+    int64_t workspace_bytes, int dtype, void* stream,
+    const AppendSpec* app) {
   const KvBlocks blocks{block_table, bt_stride_b, bt_blocks};
   EKV_REQUIRE(q && kmin && kmax && scores && k && v && page_indices && cache_seqlens && tau &&
                   out && workspace,
@@ -205,7 +216,17 @@ extern "C" int ekv_topk_paged_entmax_decode(
     return rc;
   const int n_slots = k_select + (last_page >= 0 ? 1 : 0);
   const int G = H / Hkv;
+  // the standalone append launch, ahead of any launch that reads the cache
+  auto append_first = [&]() {
+    if (!app) return (int)EKV_OK;
+    return ekv_append(app->k_new, app->v_new, app->nsb, app->nsh, const_cast<void*>(k),
+                      const_cast<void*>(v), kv_stride_b, kv_stride_h, kv_stride_row,
+                      const_cast<void*>(kmin), const_cast<void*>(kmax), app->kmean, app->kstd,
+                      s_stride_b, s_stride_h, s_stride_page, B, Hkv, D, app->pos, nullptr,
+                      block_table, bt_stride_b, bt_blocks, page_size, dtype, stream);
+  };
   auto two_launches = [&]() {
+    if (int rc = append_first()) return rc;
     int rc = ekv_page_criticality(q, q_stride_b, q_stride_h, kmin, kmax, s_stride_b, s_stride_h,
                                   s_stride_page, alibi_slopes, scores, B, H, Hkv, D, num_pages,
                                   page_size, seq_len, q_pos, k_select, last_page, seq_lens,
@@ -247,6 +268,15 @@ extern "C" int ekv_topk_paged_entmax_decode(
   t.key_cap = num_pages;
   t.seq_lens = seq_lens;
   t.prescored = 0;
+  if (app) {
+    t.app_k = app->k_new;
+    t.app_v = app->v_new;
+    t.app_nsb = app->nsb;
+    t.app_nsh = app->nsh;
+    t.app_kmean = app->kmean;
+    t.app_kstd = app->kstd;
+    t.app_pos = app->pos;
+  }
   hipStream_t s = (hipStream_t)stream;
   // fewer (b, kv head) pairs than CUs: the criticality scan, the step's
   // largest part, runs over every CU in a launch of its own, and the fused
@@ -268,6 +298,55 @@ extern "C" int ekv_topk_paged_entmax_decode(
   });
   if (rc || handled) return rc;
   return two_launches();
+}
+
+extern "C" int ekv_topk_paged_entmax_decode(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kmin, const void* kmax,
+    int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, void* scores, int num_pages,
+    int seq_len, int q_pos, int k_select, int last_page, const void* k, const void* v,
+    int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+    const int32_t* block_table, int64_t bt_stride_b, int bt_blocks,
+    int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h,
+    const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
+    const int32_t* q_seqlens, const float* alibi_slopes, const int32_t* seq_lens, float* tau,
+    int niter, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale,
+    int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens, void* workspace,
+    int64_t workspace_bytes, int dtype, void* stream) {
+  return topk_step(q, q_stride_b, q_stride_h, kmin, kmax, s_stride_b, s_stride_h, s_stride_page,
+                   scores, num_pages, seq_len, q_pos, k_select, last_page, k, v, kv_stride_b,
+                   kv_stride_h, kv_stride_row, kv_rows, block_table, bt_stride_b, bt_blocks,
+                   page_indices, pi_stride_b, pi_stride_h, cache_seqlens, cs_stride_b,
+                   cs_stride_h, q_seqlens, alibi_slopes, seq_lens, tau, niter, out, out_stride_b,
+                   out_stride_h, alpha, qscale, page_size, B, H, Hkv, D, splits, max_tokens,
+                   workspace, workspace_bytes, dtype, stream, nullptr);
+}
+
+extern "C" int ekv_append_topk_paged_entmax_decode(
+    const void* k_new, const void* v_new, int64_t new_stride_b, int64_t new_stride_h,
+    void* kmean, void* kstd, int pos,
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kmin, const void* kmax,
+    int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, void* scores, int num_pages,
+    int seq_len, int q_pos, int k_select, int last_page, const void* k, const void* v,
+    int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+    const int32_t* block_table, int64_t bt_stride_b, int bt_blocks,
+    int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h,
+    const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
+    const int32_t* q_seqlens, const float* alibi_slopes, const int32_t* seq_lens, float* tau,
+    int niter, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale,
+    int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens, void* workspace,
+    int64_t workspace_bytes, int dtype, void* stream) {
+  EKV_REQUIRE(k_new && v_new && kmean && kstd && pos >= 0 && !seq_lens,
+              "ekv_append_topk_paged_entmax_decode: null pointer, negative position or ragged "
+              "batch (use ekv_append first)");
+  EKV_REQUIRE(pos < kv_rows, "ekv_append_topk_paged_entmax_decode: row %d beyond kv_rows", pos);
+  const AppendSpec app{k_new, v_new, new_stride_b, new_stride_h, kmean, kstd, pos};
+  return topk_step(q, q_stride_b, q_stride_h, kmin, kmax, s_stride_b, s_stride_h, s_stride_page,
+                   scores, num_pages, seq_len, q_pos, k_select, last_page, k, v, kv_stride_b,
+                   kv_stride_h, kv_stride_row, kv_rows, block_table, bt_stride_b, bt_blocks,
+                   page_indices, pi_stride_b, pi_stride_h, cache_seqlens, cs_stride_b,
+                   cs_stride_h, q_seqlens, alibi_slopes, seq_lens, tau, niter, out, out_stride_b,
+                   out_stride_h, alpha, qscale, page_size, B, H, Hkv, D, splits, max_tokens,
+                   workspace, workspace_bytes, dtype, stream, &app);
 }
 
 extern "C" int ekv_gaussian_paged_entmax_decode(

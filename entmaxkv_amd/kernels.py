@@ -38,6 +38,17 @@ class KVBlocks(NamedTuple):
     num_blocks: int
 
 
+class AppendRow(NamedTuple):
+    """One row appended by the top-k step itself: k_new, v_new [B, Hkv, D]
+    at row ``pos`` of every sequence, with the mean/std statistics views
+    (min/max are the step's own k_min/k_max)."""
+    k_new: torch.Tensor
+    v_new: torch.Tensor
+    k_mean: torch.Tensor
+    k_std: torch.Tensor
+    pos: int
+
+
 def _bt_args(blocks: "KVBlocks | None"):
     if blocks is None:
         return (None, 0, 0)
@@ -266,12 +277,15 @@ def topk_paged_entmax_decode(q, k_min, k_max, scores, k_select: int, last_page: 
                              workspace: DecodeWorkspace | None = None, kv_rows: int | None = None,
                              taus_out: torch.Tensor | None = None,
                              blocks: KVBlocks | None = None,
-                             seq_lens: torch.Tensor | None = None):
+                             seq_lens: torch.Tensor | None = None,
+                             append: AppendRow | None = None):
     """Criticality + top-k + exact-tau decode of one step (ekv_topk_paged_entmax_decode).
 
     Scores the pages [0, scores.shape[2]) into ``scores``, writes the top-k page
     table (last page at slot k) into ``page_indices`` [B, Hkv, k + 1] and the
     decode output into ``out``; a single launch when the shape allows it.
+    With ``append`` the row is appended first, inside the same launch when it
+    is fused (ekv_append_topk_paged_entmax_decode; uniform batches only).
     """
     require_gpu(q, k_min, k_max, scores, k_cache, v_cache, out, page_indices)
     batch, nheads, q_len, dim = q.shape
@@ -313,7 +327,21 @@ def topk_paged_entmax_decode(q, k_min, k_max, scores, k_select: int, last_page: 
         qsl = q_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
     if kv_rows is None:
         kv_rows = k_cache.shape[2] if blocks is None else blocks.table.shape[1] * page_size
-    call("ekv_topk_paged_entmax_decode",
+    head = ()
+    name = "ekv_topk_paged_entmax_decode"
+    if append is not None:
+        if seq_lens is not None:
+            raise ValueError("a fused append needs a uniform batch")
+        kn = _row_major_d(append.k_new, "k_new")
+        vn = _row_major_d(append.v_new, "v_new")
+        if kn.stride() != vn.stride():
+            kn, vn = kn.contiguous(), vn.contiguous()
+        if append.k_mean.stride() != k_min.stride() or append.k_std.stride() != k_min.stride():
+            raise ValueError("k_mean and k_std must share k_min's strides")
+        head = (kn.data_ptr(), vn.data_ptr(), kn.stride(0), kn.stride(1),
+                append.k_mean.data_ptr(), append.k_std.data_ptr(), int(append.pos))
+        name = "ekv_append_topk_paged_entmax_decode"
+    call(name, *head,
          q3.data_ptr(), q3.stride(0), q3.stride(1), k_min.data_ptr(), k_max.data_ptr(),
          k_min.stride(0), k_min.stride(1), k_min.stride(2), scores.data_ptr(), num_pages,
          seq_len, q_pos, k_select, last_page, k_cache.data_ptr(), v_cache.data_ptr(),

@@ -334,6 +334,30 @@ class PagedKVCache:
         else:
             self.seq_len = pos + 1
 
+    def reserve_append(self, k_new: torch.Tensor, v_new: torch.Tensor) -> "K.AppendRow":
+        """The host side of ``append`` for a uniform batch and one token: the
+        row is reserved (capacity, block), ``seq_len`` counts it, and the
+        returned row is written by the next top-k step's launch
+        (``kernels.topk_paged_entmax_decode(append=...)``) or by
+        ``write_append``."""
+        if self.seq_lens is not None or k_new.shape[2] != 1:
+            raise ValueError("reserve_append: uniform batch and one token only")
+        pos = self.seq_len
+        if self.block_pool:
+            self._assign_append_blocks(pos)
+        elif pos + 1 > self.kv_capacity:
+            self._grow(pos + 1 + self.headroom)
+        self.seq_len = pos + 1
+        return K.AppendRow(k_new[:, :, 0], v_new[:, :, 0], self._moments[:, :, :, 0],
+                           self._moments[:, :, :, 1], pos)
+
+    def write_append(self, row: "K.AppendRow") -> None:
+        """Writes a row reserved by ``reserve_append`` with its own launch."""
+        blocks = K.KVBlocks(self._table, self._k.shape[0]) if self.block_pool else None
+        K.append_token(row.k_new, row.v_new, self._k, self._v, self._bounds[:, :, :, 0],
+                       self._bounds[:, :, :, 1], row.k_mean, row.k_std, row.pos,
+                       self.page_size, blocks=blocks)
+
     # ---------------------------------------------------------- criticality
     def estimate_page_criticality(self, q: torch.Tensor, use_triton: bool = False,
                                   alibi_slopes=None, q_pos: int = 0,

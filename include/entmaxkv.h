@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define EKV_ABI_VERSION 4
+#define EKV_ABI_VERSION 5
 
 const char* ekv_last_error(void);
 int ekv_abi_version(void);
@@ -128,6 +128,30 @@ int ekv_paged_entmax_decode(const void* q, int64_t q_stride_b, int64_t q_stride_
  * Replaces the selection + decode sequence of sparse_attention_decode_paged,
  * attention_topk.py:45-98. */
 int ekv_topk_paged_entmax_decode(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kmin, const void* kmax,
+    int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, void* scores, int num_pages,
+    int seq_len, int q_pos, int k_select, int last_page, const void* k, const void* v,
+    int64_t kv_stride_b, int64_t kv_stride_h, int64_t kv_stride_row, int64_t kv_rows,
+    const int32_t* block_table, int64_t bt_stride_b, int bt_blocks,
+    int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h,
+    const int32_t* cache_seqlens, int64_t cs_stride_b, int64_t cs_stride_h,
+    const int32_t* q_seqlens, const float* alibi_slopes, const int32_t* seq_lens, float* tau,
+    int niter, void* out, int64_t out_stride_b, int64_t out_stride_h, float alpha, float qscale,
+    int page_size, int B, int H, int Hkv, int D, int splits, int max_tokens, void* workspace,
+    int64_t workspace_bytes, int dtype, void* stream);
+
+/* ekv_append followed by ekv_topk_paged_entmax_decode, the step of
+ * sparse_attention_decode_paged with append_cache=True (attention_topk.py:
+ * 45-47 then 52-98, kv_cache.py:72-116): row `pos` of K and V comes from
+ * k_new / v_new [B, Hkv, D] (row strides new_stride_b, new_stride_h) and the
+ * statistics of page pos / page_size are recomputed (kmean, kstd with the
+ * strides of kmin, kmax).  seq_len, q_pos, cache_seqlens and kv_rows already
+ * count the new row.  Uniform batches only (seq_lens null).  In the fused
+ * launch the append runs inside the top-k kernel (its page is the last one,
+ * which the criticality scan never reads), else as its own launch first. */
+int ekv_append_topk_paged_entmax_decode(
+    const void* k_new, const void* v_new, int64_t new_stride_b, int64_t new_stride_h,
+    void* kmean, void* kstd, int pos,
     const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* kmin, const void* kmax,
     int64_t s_stride_b, int64_t s_stride_h, int64_t s_stride_page, void* scores, int num_pages,
     int seq_len, int q_pos, int k_select, int last_page, const void* k, const void* v,
