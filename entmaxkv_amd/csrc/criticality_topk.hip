@@ -55,7 +55,7 @@ __global__ __launch_bounds__(kHeadThreads) void criticality_head_kernel(
     int page_size, int seq_len, int q_pos, int k_sel, int last_page,
     const int32_t* __restrict__ seq_lens, int32_t* page_indices, int64_t pisb, int64_t pish,
     int lds_key_cap, int list_words) {
-  extern __shared__ uint32_t lds_keys[];
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds_keys[];
   const int bkv = blockIdx.x;
   const int b = bkv / Hkv, kvh = bkv % Hkv;
   const Ragged r = ragged_topk(seq_lens, b, page_size, stride, seq_len, q_pos, k_sel, last_page);
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const T* __restrict__ sc
   const int b = bkv / Hkv, kvh = bkv % Hkv;
   const Ragged r = ragged_topk(seq_lens, b, page_size, stride, 0, 0, k, last_page);
   const T* s0 = scores + ((int64_t)b * H + kvh * G) * stride;
-  extern __shared__ uint32_t lds_keys[];
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds_keys[];
   topk_select_block<T, G, kThreads>(s0, stride, r.count, r.k, r.last_page,
                                     page_indices + b * pisb + kvh * pish, lds_keys, lds_key_cap,
                                     false, nullptr, lds_keys + stride, nullptr, 0, list_words);

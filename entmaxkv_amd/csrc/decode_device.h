@@ -1091,7 +1091,7 @@ template <typename T, int LPR, int G, int U>
 __global__ __launch_bounds__(kHeadThreads) void decode_head_kernel(DecodeArgs a) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int D = LPR * VEC;
-  extern __shared__ float stage[];  // [G][stage_cap] scores when staged
+  extern __shared__ __attribute__((aligned(16))) float stage[];  // [G][stage_cap] scores when staged
   __shared__ __attribute__((aligned(16))) int hist[kWaves][kBins];
   __shared__ float4 part[2 * kWaves];
   __shared__ float s_tau[G];
@@ -1151,7 +1151,7 @@ template <typename T, int LPR, int G, int UC, int UD>
 __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a, SelectArgs t) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int D = LPR * VEC;
-  extern __shared__ float stage[];
+  extern __shared__ __attribute__((aligned(16))) float stage[];
   __shared__ __attribute__((aligned(16))) int hist[kWaves][kBins];
   __shared__ float4 part[2 * kWaves];
   __shared__ float s_tau[G];
@@ -1176,7 +1176,7 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
     for (int i = threadIdx.x; i < (int)(sizeof(sel_hist) / 4); i += kHeadThreads)
       (&sel_hist[0][0])[i] = 0u;
   }
-  __syncthreads();
+  if (G == 1 || !t.prescored) __syncthreads();
   if (t.app_k && threadIdx.x < LPR) {
     // the appended row and its page's statistics: the page is the last one,
     // which the scan never reads; the K/V phases read the row after the
@@ -1204,7 +1204,7 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
   EKV_STAMP(0);
   const T* sbase = (const T*)t.scores + ((int64_t)b * a.H + kvh * G) * t.num_pages;
   if (!t.prescored) {
-    topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC>(
+    topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC, true>(
         (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
         a.slopes, (T*)t.scores, a.H, t.num_pages, r.count, a.page_size, r.seq_len, r.q_pos, b,
         kvh, G == 1 ? (keep ? keys : nullptr) : head_keys,
@@ -1301,7 +1301,7 @@ template <typename T, int LPR, int G, int UD>
 __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArgs a, GaussArgs f) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int D = LPR * VEC;
-  extern __shared__ float stage[];
+  extern __shared__ __attribute__((aligned(16))) float stage[];
   __shared__ __attribute__((aligned(16))) int hist[kWaves][kBins];
   __shared__ float4 part[2 * kWaves];
   __shared__ float s_tau[G];

@@ -788,7 +788,7 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
 // row segment of LPR lanes owns one page and loads its min and max rows with
 // 16-byte loads, U pages per segment in flight.  Returns the head's score
 // base pointer.
-template <typename T, int LPR, int G, int NT, int U>
+template <typename T, int LPR, int G, int NT, int U, bool kChunked = false>
 __device__ __forceinline__ T* criticality_scan_head(
     const T* __restrict__ q, int64_t qsb, int64_t qsh, const T* __restrict__ kmin,
     const T* __restrict__ kmax, int64_t ssb, int64_t ssh, int64_t ssp,
@@ -854,7 +854,7 @@ __device__ __forceinline__ T* criticality_scan_head(
       }
     }
   };
-  if (lds_next) {
+  if constexpr (kChunked) {
     // waves take chunks of U * (64 / LPR) consecutive pages from a shared
     // counter (zero and visible on entry), the next chunk's index fetched
     // while the current chunk's loads are in flight: a wave slowed by its
