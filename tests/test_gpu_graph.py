@@ -89,3 +89,41 @@ def test_gaussian_step_graph_replay(B, Hkv, G, tau_mode):
     step()
     torch.cuda.synchronize()
     _replays_match(step, [out, cache.last_num_selected_per_head])
+
+
+@pytest.mark.parametrize("shape", [(2, 2, 4, 400, 100, "bf16"), (8, 16, 1, 300, 64, "fp16")])
+def test_noalloc_step_graph_replay(shape):
+    """ekv_topk_paged_entmax_decode_noalloc, the entry point for code under
+    graph capture (its workspace is the library's static scratch)."""
+    from entmaxkv_amd import _lib
+    from entmaxkv_amd.kernels import choose_splits, qscale_for
+    from tests.test_zz_no_alloc import _case as noalloc_case
+    B, Hkv, G, pages, k, dtype = shape
+    _case(test="graph_noalloc", B=B, Hkv=Hkv, G=G, pages=pages, k=k, dtype=dtype)
+    c = noalloc_case(B, Hkv, G, pages, k, dtype, 11)
+    dev = c["q"].device
+    H, D, ps, P = c["H"], c["D"], c["ps"], c["P"]
+    dt = TORCH_DT[dtype]
+    n_slots = k + 1
+    max_tokens = n_slots * ps
+    scores = torch.zeros((B, H, P - 1), dtype=dt, device=dev)
+    pidx = torch.zeros((B, Hkv, n_slots), dtype=torch.int32, device=dev)
+    seqlens = torch.full((B, Hkv), k * ps + c["lps"], dtype=torch.int32, device=dev)
+    tau = torch.zeros((B, H), dtype=torch.float32, device=dev)
+    out = torch.zeros((B, H, D), dtype=dt, device=dev)
+    q3 = c["q"][:, :, 0]
+    cache = c["cache"]
+    kmin, kmax, kc, vc = cache.k_min, cache.k_max, cache._k, cache._v
+    args = [q3.data_ptr(), q3.stride(0), q3.stride(1), kmin.data_ptr(), kmax.data_ptr(),
+            kmin.stride(0), kmin.stride(1), kmin.stride(2), scores.data_ptr(), P - 1, c["S"],
+            c["S"] - 1, k, P - 1, kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1),
+            kc.stride(2), kc.shape[2], None, 0, 0, pidx.data_ptr(), pidx.stride(0),
+            pidx.stride(1), seqlens.data_ptr(), seqlens.stride(0), seqlens.stride(1), None,
+            None, None, tau.data_ptr(), 2, out.data_ptr(), out.stride(0), out.stride(1), 1.5,
+            qscale_for(1.5, D, dt), ps, B, H, Hkv, D, choose_splits(max_tokens), max_tokens,
+            {"fp32": 0, "fp16": 1, "bf16": 2}[dtype]]
+
+    def step():
+        _lib.call("ekv_topk_paged_entmax_decode_noalloc", *args,
+                  torch.cuda.current_stream(dev).cuda_stream)
+    _replays_match(step, [out, pidx, tau, scores])
