@@ -1,11 +1,11 @@
 """Decode-step benchmark of the EntmaxKV MI355X build.
 
-Workload (BASELINE metric): B=8, H=32 (MHA), D=128, 32768-token prefill plus one
+Workload (the headline metric): B=8, H=32 (MHA), D=128, 32768-token prefill plus one
 appended token, page size 16, fp16, alpha=1.5.  One step = one call of
 ``sparse_attention_decode_paged`` (token budget 1024, niter 2, the cache
 already appended, as in the reference's tests/run_benchmarks.py), with every
 input resident in HBM.  The Gaussian-aware step (tau_mode "corrected") on the
-same shape is reported alongside, on keys drawn as in BASELINE config 3
+same shape is reported alongside, on keys drawn as in benchmark config 3
 (per-head offsets, 2% outlier pages aligned with q; --gauss-keys iid for N(0, 1)).
 
 value = effective bytes per step / step time, where the effective bytes are
@@ -50,11 +50,11 @@ def _args():
     p.add_argument("--no-gaussian", action="store_true")
     p.add_argument("--gauss-keys", choices=["c3", "iid"], default="c3",
                    help="keys of the Gaussian-aware step: c3 = N(mu_h, 1) per head with 2%% "
-                        "outlier pages scaled x3 toward q (BASELINE config 3), iid = N(0, 1)")
+                        "outlier pages scaled x3 toward q (benchmark config 3), iid = N(0, 1)")
     p.add_argument("--only", choices=["topk", "gaussian", "criticality"], default=None,
                    help="run one step kind in a loop (for profilers)")
     p.add_argument("--config", choices=["headline", "c5", "dense", "rows"], default="headline",
-                   help="c5: BASELINE config 5 instead of the headline line (ragged batch, "
+                   help="c5: benchmark config 5 instead of the headline line (ragged batch, "
                         "B=32, 32 q / 8 kv heads, bf16, lengths ~ U[4096, 131072], 1%% outlier "
                         "pages x4, Gaussian alpha 1.5 with append over 16 consecutive steps); "
                         "dense: the dense (non-paged) decode over every token of the headline "
@@ -127,7 +127,7 @@ def _gaussian_cache(B, H, Hkv, L, D, ps, dt, dev, q, kind):
 
 
 def _config5(a):
-    """a ragged batch decoded with Gaussian-aware selection.
+    """benchmark config 5: a ragged batch decoded with Gaussian-aware selection.
 
     B=32, H=32 query / 8 kv heads, D=128, bf16, page size 16; sequence
     lengths drawn from U[4096, 131072] (seeded, last pages partial); keys and
@@ -196,7 +196,7 @@ def _config5(a):
     step_bytes = stat_bytes + sel_tok * D * esz * 2 + 2 * B * H * D * esz + 2 * B * Hkv * D * esz
     gbs = step_bytes / (ms * 1e-3) / 1e9
     print(json.dumps({
-        "metric": "decode-step us + effective KV GB/s (% HBM peak), BASELINE config 5",
+        "metric": "decode-step us + effective KV GB/s (% HBM peak), benchmark config 5",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": n_steps,
         "warmup": a.warmup, "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2), "higher_is_better": True,

@@ -365,7 +365,7 @@ constexpr int kLdsPerWorkgroup = 160 * 1024;
 // The fused one-workgroup-per-(b, kv head) launches win when there are at
 // least half as many heads as compute units: below that, a head's scan spread
 // over many workgroups finishes sooner.  Measured at 128 heads on 256 CUs
-// (BASELINE configs 3 and 4) the fused launches are faster for the top-k step
+// (benchmark configs 3 and 4) the fused launches are faster for the top-k step
 // and for Gaussian selections of tens of pages, slower by 30 % for a
 // Gaussian selection of half the cache.  Ragged batches always split: one
 // workgroup per head would wait on the longest sequence.

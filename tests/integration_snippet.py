@@ -1,4 +1,4 @@
-"""Loads the reference-side ctypes binding that INTEGRATION.md gives, as a module.
+"""Loads the reference-side ctypes binding that the integration guide gives, as a module.
 
 The block is the text a maintainer would paste into the reference package as
 ``entmaxkv/kernels/_amd.py``; running it from the document keeps the document
@@ -18,7 +18,7 @@ def snippet_source() -> str:
     txt = open(DOC).read()
     blocks = re.findall(r"```python\n(.*?)```", txt, flags=re.S)
     found = [b for b in blocks if b.startswith(MARK)]
-    assert len(found) == 1, "INTEGRATION.md must hold exactly one reference-side binding block"
+    assert len(found) == 1, "the integration guide must hold exactly one reference-side binding block"
     return found[0]
 
 

@@ -59,7 +59,7 @@ def test_missing_library_raises(monkeypatch, tmp_path):
 
 
 def test_integration_snippet_matches_the_abi():
-    """The reference-side ctypes block of INTEGRATION.md declares, and passes,
+    """The integration guide's reference-side ctypes block declares, and passes,
     exactly the parameters of ekv_page_criticality."""
     import ast
     import ctypes

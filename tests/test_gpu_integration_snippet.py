@@ -1,4 +1,4 @@
-"""Runs the reference-side ctypes binding of INTEGRATION.md on the GPU and
+"""Runs the integration guide's reference-side ctypes binding on the GPU and
 compares its scores with entmaxkv_amd's own criticality launcher and with the
 oracle (kernels/page_criticality.py:107-187 is the interface it replaces)."""
 

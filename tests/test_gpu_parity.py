@@ -384,7 +384,7 @@ def test_topk_api_end_to_end(dtype, G, path, alibi):
 
 
 def test_config1_topk_step():
-    """BASELINE config 1 on the GPU: B=1, H=32, D=128, 1024-token prefill + one
+    """benchmark config 1 on the GPU: B=1, H=32, D=128, 1024-token prefill + one
     appended token, page size 16, fp32, budget 256, alpha 1.5 (niter 10): the
     page table equals the oracle's top-k of the kernel's scores and the output
     equals the oracle step within 1e-5."""
@@ -417,7 +417,7 @@ def test_config1_topk_step():
 
 @pytest.mark.parametrize("path,niter", [("head", 2), ("head", 10), ("split", 10)])
 def test_config4_topk_step(path, niter):
-    """BASELINE config 4's top-k step at a shorter length: 32 query / 8 kv
+    """benchmark config 4's top-k step at a shorter length: 32 query / 8 kv
     heads (G = 4), D = 128, bf16, alpha = 2 (sparsemax), budget 2048 tokens
     (128 pages + the last page per kv head), one appended token, q/k/v ~ N(0, 1).
     "head": B = 16 as in the config (one fused launch per step, prescored);

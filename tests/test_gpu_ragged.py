@@ -1,7 +1,7 @@
 """Ragged batches (per-sequence lengths) on the GPU against the oracle.
 
 The reference cache holds one length (kv_cache.py:23-38), so a ragged batch
-is this build's extension.  It is pinned by per-sequence
+is this build's extension (benchmark config 5).  It is pinned by per-sequence
 decomposition: every sequence must give what the oracle gives for that
 sequence alone, except for the batch-wide automatic margins of the Gaussian
 selection, which are formed from every head of the batch as in the uniform

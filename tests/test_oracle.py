@@ -522,7 +522,7 @@ def test_given_tau_zero_iters_is_plain_weighted_sum():
 
 
 def test_config1_cpu_topk_step():
-    """BASELINE config 1 (the reference's CPU-sized case): B=1, H=32, D=128, a
+    """benchmark config 1 (the reference's CPU-sized case): B=1, H=32, D=128, a
     1024-token prefill plus one decode token, page size 16, fp32, budget 256,
     alpha 1.5.  Parity: the step equals exact entmax-1.5 over the 257 selected
     tokens.  Against dense entmax-1.5 over all 1025 tokens the relative L2 gap is
