@@ -26,17 +26,20 @@ def _same(a, b, what):
     assert torch.equal(a, b), f"{what}: fused append differs from append + step"
 
 
-@pytest.mark.parametrize("B,Hkv,G,dtype,pool,budget", [
-    (8, 32, 1, "fp16", False, 256),   # fused scan (B * Hkv = 256)
-    (4, 32, 1, "fp16", False, 256),   # prescored (128)
-    (16, 8, 4, "bf16", False, 512),   # GQA, prescored
-    (2, 2, 2, "fp32", False, 128),    # split launches (the append runs first)
-    (8, 16, 1, "bf16", True, 256),    # block pool
-    (4, 4, 2, "fp16", False, 8),      # budget below a page: no selection
+@pytest.mark.parametrize("B,Hkv,G,dtype,pool,budget,alibi", [
+    (8, 32, 1, "fp16", False, 256, False),   # fused scan (B * Hkv = 256)
+    (8, 32, 1, "fp16", False, 256, True),    # ALiBi
+    (4, 32, 1, "fp16", False, 256, False),   # prescored (128)
+    (16, 8, 4, "bf16", False, 512, False),   # GQA, prescored
+    (2, 2, 2, "fp32", False, 128, False),    # split launches (the append runs first)
+    (2, 2, 2, "fp32", False, 128, True),     # split launches, ALiBi
+    (8, 16, 1, "bf16", True, 256, False),    # block pool
+    (4, 4, 2, "fp16", False, 8, False),      # budget below a page: no selection
 ])
-def test_fused_append_matches_append_then_step(B, Hkv, G, dtype, pool, budget):
+def test_fused_append_matches_append_then_step(B, Hkv, G, dtype, pool, budget, alibi):
     from entmaxkv_amd import PagedKVCache, sparse_attention_decode_paged
-    _case(test="fused_append", B=B, Hkv=Hkv, G=G, dtype=dtype, pool=pool, budget=budget)
+    _case(test="fused_append", B=B, Hkv=Hkv, G=G, dtype=dtype, pool=pool, budget=budget,
+          alibi=alibi)
     rng = np.random.default_rng(700 + B + G)
     S, D = 16 * 24 - 2, 128  # the second append completes a page, the third opens one
     H = Hkv * G
@@ -50,15 +53,19 @@ def test_fused_append_matches_append_then_step(B, Hkv, G, dtype, pool, budget):
         c.initialize(to_dev(k, dtype), to_dev(v, dtype))
         caches.append(c)
     fused, ref = caches
+    slopes = (torch.tensor([2.0 ** (-8.0 * (h + 1) / H) for h in range(H)], device="cuda")
+              if alibi else None)
     for step in range(5):
         kn = to_dev(randn(rng, (B, Hkv, 1, D), dtype), dtype)
         vn = to_dev(randn(rng, (B, Hkv, 1, D), dtype), dtype)
         outs = [torch.zeros(B, H, 1, D, dtype=TORCH_DT[dtype], device="cuda") for _ in range(2)]
-        sparse_attention_decode_paged(q, fused, kn, vn, outs[0], budget, None, None, alpha=1.5,
-                                      niter=2, append_cache=True)
+        sparse_attention_decode_paged(q, fused, kn, vn, outs[0], budget, None, None,
+                                      alibi_slopes=slopes, alpha=1.5, niter=2,
+                                      append_cache=True)
         ref.append(kn, vn)
-        sparse_attention_decode_paged(q, ref, None, None, outs[1], budget, None, None, alpha=1.5,
-                                      niter=2, append_cache=False)
+        sparse_attention_decode_paged(q, ref, None, None, outs[1], budget, None, None,
+                                      alibi_slopes=slopes, alpha=1.5, niter=2,
+                                      append_cache=False)
         assert fused.seq_len == ref.seq_len == S + step + 1
         _same(outs[0], outs[1], f"out step {step}")
         _same(fused._page_indices_buf, ref._page_indices_buf, f"page table step {step}")
