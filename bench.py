@@ -80,6 +80,21 @@ def _time_loop(fn, steps, warmup, stream):
     return start.elapsed_time(end) / steps  # ms
 
 
+def _step_percentiles(fn, steps, stream):
+    """Median and 90th percentile of single-step durations (us), each step
+    bracketed by its own events (after the timed loops, not part of them)."""
+    import torch
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for s, e in ev:
+        s.record(stream)
+        fn()
+        e.record(stream)
+    torch.cuda.synchronize()
+    t = sorted(s.elapsed_time(e) * 1e3 for s, e in ev)
+    return round(t[len(t) // 2], 2), round(t[(9 * len(t)) // 10], 2)
+
+
 def _graphed(fn, stream):
     import torch
     g = torch.cuda.CUDAGraph()
@@ -434,6 +449,7 @@ def main():
         "us_per_step": round(ms * 1e3, 2),
         "us_per_step_eager": round(ms_eager * 1e3, 2),
         "us_per_step_graph": None if ms_graph is None else round(ms_graph * 1e3, 2),
+        "us_step_median_p90": _step_percentiles(topk_step, min(a.steps, 200), stream),
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "higher_is_better": True,
         "scaling": "weak",
