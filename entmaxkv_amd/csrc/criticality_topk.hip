@@ -80,13 +80,19 @@ __global__ __launch_bounds__(kThreads) void criticality_kernel(
     const T* __restrict__ q, int64_t qsb, int64_t qsh, const T* __restrict__ kmin,
     const T* __restrict__ kmax, int64_t ssb, int64_t ssh, int64_t ssp,
     const float* __restrict__ slopes, T* __restrict__ scores, int H, int Hkv, int stride,
-    int page_size, int seq_len_all, int q_pos_all, const int32_t* __restrict__ seq_lens) {
+    int page_size, int seq_len_all, int q_pos_all, const int32_t* __restrict__ seq_lens,
+    int rev) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int SEGS = kThreads / LPR;
+  // rev: the workgroups take their (b, kv head, page round) in the opposite
+  // order of their dispatch, last first
+  const int lin = blockIdx.y * gridDim.x + blockIdx.x;
+  const int wg = rev ? gridDim.x * gridDim.y - 1 - lin : lin;
+  const int wx = wg % gridDim.x;
   const int seg = threadIdx.x / LPR;
   const int sl = threadIdx.x % LPR;
   const int col = sl * VEC;
-  const int bkv = blockIdx.y;
+  const int bkv = wg / gridDim.x;
   const int b = bkv / Hkv, kvh = bkv % Hkv;
   const int h0 = kvh * G;
   const Ragged r = ragged_topk(seq_lens, b, page_size, stride, seq_len_all, q_pos_all, -1, -1);
@@ -99,8 +105,8 @@ __global__ __launch_bounds__(kThreads) void criticality_kernel(
   }
   const T* kmn = kmin + b * ssb + kvh * ssh;
   const T* kmx = kmax + b * ssb + kvh * ssh;
-  const int p_base = blockIdx.x * (SEGS * kUnroll) + seg;
-  if (blockIdx.x * (SEGS * kUnroll) >= num_pages) return;  // past this sequence's pages
+  const int p_base = wx * (SEGS * kUnroll) + seg;
+  if (wx * (SEGS * kUnroll) >= num_pages) return;  // past this sequence's pages
   // unconditional loads (a page past the end re-reads the last one, its
   // result is discarded) so that all of them are in flight together
   uint4 lo[kUnroll], hi[kUnroll];
@@ -243,7 +249,7 @@ extern "C" int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q
         hipLaunchKernelGGL((criticality_kernel<T, LPR, G>), grid, dim3(kThreads), 0, s, (const T*)q,
                            q_stride_b, q_stride_h, (const T*)kmin, (const T*)kmax, s_stride_b,
                            s_stride_h, s_stride_page, alibi_slopes, (T*)scores, H, Hkv, num_pages,
-                           page_size, seq_len, q_pos, seq_lens);
+                           page_size, seq_len, q_pos, seq_lens, next_scan_order());
         if (k_select >= 0) {
           int rc = check_launch("criticality_kernel");
           if (rc) return rc;
@@ -268,7 +274,7 @@ int criticality_split_scores(const void* q, int64_t q_stride_b, int64_t q_stride
                              int64_t s_stride_h, int64_t s_stride_page,
                              const float* alibi_slopes, void* scores, int B, int H, int Hkv,
                              int D, int num_pages, int page_size, int seq_len, int q_pos,
-                             const int32_t* seq_lens, int dtype, hipStream_t s) {
+                             const int32_t* seq_lens, int dtype, hipStream_t s, int rev) {
   return dispatch_dtype(dtype, [&](auto tv) {
     using T = decltype(tv);
     return dispatch_lpr<T>(D, [&](auto lpr) {
@@ -280,7 +286,8 @@ int criticality_split_scores(const void* q, int64_t q_stride_b, int64_t q_stride
         hipLaunchKernelGGL((criticality_kernel<T, LPR, G>), grid, dim3(kThreads), 0, s,
                            (const T*)q, q_stride_b, q_stride_h, (const T*)kmin,
                            (const T*)kmax, s_stride_b, s_stride_h, s_stride_page, alibi_slopes,
-                           (T*)scores, H, Hkv, num_pages, page_size, seq_len, q_pos, seq_lens);
+                           (T*)scores, H, Hkv, num_pages, page_size, seq_len, q_pos, seq_lens,
+                           rev);
         return check_launch("criticality_kernel");
       });
     });

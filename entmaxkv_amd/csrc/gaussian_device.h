@@ -215,6 +215,7 @@ struct MomentsArgs {
   float* sigma_p;       // [B, H, pages]
   float4* partials;     // [B, H, splits] (Sum mu, Sum mu^2, Sum var, 0)
   const int32_t* seq_lens;  // [B] per-sequence lengths (ragged batch) or null
+  int rev = 0;              // LDS-staged scans take their rounds last first
 };
 
 // Moments of pages [split * pages_per_split, ...) of one (b, kv head) for its
@@ -224,7 +225,10 @@ struct MomentsArgs {
 // and the workgroup's partial sums (of the unbiased mu_p).  A row segment of
 // LPR lanes owns a page; U pages per segment in flight.  blockDim == NT.
 // Page moments of one workgroup staged in LDS (kLdsOut) before one coalesced
-// write-out per head after the scan, when pages_per_split * G fits.
+// write-out per head after the scan, when pages_per_split * G fits.  The
+// workgroup's partial sums are then formed from LDS in page order, so that
+// they do not depend on the order of the scan, which alternates from launch
+// to launch (a.rev) like the criticality scan's.
 constexpr int kMomentLdsEntries = 4096;
 
 template <typename T, int LPR, int G, int NT, int U, bool kLdsOut = false>
@@ -305,25 +309,30 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
         float mu = 0.f, var = 0.f;
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          const float w = sv[u].get(i) * qa[g][i];
-          mu += mv[u].get(i) * qs[g][i];
-          var += w * w;
+          // explicit roundings: both register buffers' inlined copies of this
+          // loop give the same bits (the scan order alternates between them)
+          const float w = mul_rn(sv[u].get(i), qa[g][i]);
+          mu = fma_rn(mv[u].get(i), qs[g][i], mu);
+          var = fma_rn(w, w, var);
         }
         mu = seg_sum<LPR>(mu);
         var = seg_sum<LPR>(var);
-        s_mu[g] += acc ? mu : 0.f;
-        s_mu2[g] += acc ? mu * mu : 0.f;
-        s_var[g] += acc ? var : 0.f;
+        if constexpr (!kLdsOut) {
+          s_mu[g] += acc ? mu : 0.f;
+          s_mu2[g] += acc ? mu * mu : 0.f;
+          s_var[g] += acc ? var : 0.f;
+        }
         const int64_t o = ((int64_t)b * a.H + h0 + g) * a.pages + pc;
         float mub = mu;
-        if (a.slopes) {
+        if (!kLdsOut && a.slopes) {
           // gaussian_utils.py:142-153: slope * (min(p*ps + (ps-1)/2, S'-1) - q_pos)
           const float pos = fminf((float)pc * (float)a.page_size + (float)(a.page_size - 1) * 0.5f,
                                   (float)(stats_len - 1));
           mub = add_rn(mu, mul_rn(slope[g], sub_rn(pos, (float)q_pos)));
         }
         if constexpr (kLdsOut) {
-          if (sl == 0) lds_out[(pc - p_begin) * G + g] = make_float2(mub, sqrtf(var));
+          // the raw moments; the bias, the root and the sums come after the scan
+          if (sl == 0) lds_out[(pc - p_begin) * G + g] = make_float2(mu, var);
         } else {
           a.mu_p[o] = mub;
           a.sigma_p[o] = sqrtf(var);
@@ -332,14 +341,46 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
     }
   };
   if (p_begin < p_end) {
+    // round k of nr starts at page start(k); reversed, the last round first
+    // (a round past either end re-reads clamped pages and discards them)
+    const int nr = (p_end - p_begin + ROUND - 1) / ROUND;
+    const bool rev = kLdsOut && a.rev;
+    auto start = [&](int k) { return p_begin + (rev ? nr - 1 - k : k) * ROUND; };
     VecRaw<T> mv_a[U], sv_a[U], mv_b[U], sv_b[U];
-    fetch(p_begin, mv_a, sv_a);
-    for (int p0 = p_begin; p0 < p_end; p0 += 2 * ROUND) {
-      fetch(p0 + ROUND, mv_b, sv_b);
-      consume(p0, mv_a, sv_a);
-      if (p0 + ROUND >= p_end) break;
-      fetch(p0 + 2 * ROUND, mv_a, sv_a);
-      consume(p0 + ROUND, mv_b, sv_b);
+    fetch(start(0), mv_a, sv_a);
+    for (int k = 0; k < nr; k += 2) {
+      fetch(k + 1 < nr ? start(k + 1) : p_end, mv_b, sv_b);
+      consume(start(k), mv_a, sv_a);
+      if (k + 1 >= nr) break;
+      fetch(k + 2 < nr ? start(k + 2) : p_end, mv_a, sv_a);
+      consume(start(k + 1), mv_b, sv_b);
+    }
+  }
+  if constexpr (kLdsOut) {
+    // page moments out (with the ALiBi page-mean bias and the root), and the
+    // partial sums of the unbiased mu_p in page order, thread j taking pages
+    // j, j + NT, ...
+    __syncthreads();
+    const int np = max(p_end - p_begin, 0);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t o = ((int64_t)b * a.H + h0 + g) * a.pages + p_begin;
+      for (int j = threadIdx.x; j < np; j += NT) {
+        const float2 v = lds_out[j * G + g];
+        float mub = v.x;
+        if (a.slopes) {
+          // gaussian_utils.py:142-153: slope * (min(p*ps + (ps-1)/2, S'-1) - q_pos)
+          const float pos = fminf((float)(p_begin + j) * (float)a.page_size +
+                                      (float)(a.page_size - 1) * 0.5f,
+                                  (float)(stats_len - 1));
+          mub = add_rn(v.x, mul_rn(slope[g], sub_rn(pos, (float)q_pos)));
+        }
+        a.mu_p[o + j] = mub;
+        a.sigma_p[o + j] = sqrtf(v.y);
+        s_mu[g] += v.x;
+        s_mu2[g] += v.x * v.x;
+        s_var[g] += v.y;
+      }
     }
   }
   // workgroup partials in a fixed order: lanes, then waves
@@ -359,19 +400,6 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
       r.z += red[g][w].z;
     }
     a.partials[((int64_t)b * a.H + h0 + g) * a.splits + split] = r;
-  }
-  if constexpr (kLdsOut) {
-    // the barrier above also ordered every lds_out write before these reads
-    const int np = max(p_end - p_begin, 0);
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int64_t o = ((int64_t)b * a.H + h0 + g) * a.pages + p_begin;
-      for (int j = threadIdx.x; j < np; j += NT) {
-        const float2 v = lds_out[j * G + g];
-        a.mu_p[o + j] = v.x;
-        a.sigma_p[o + j] = v.y;
-      }
-    }
   }
 }
 

@@ -19,6 +19,8 @@
 // Under GQA (H = G * Hkv) every query head keeps its own moments, tau-hat and
 // tau floor; the page table of a kv head is the union of its query heads'
 // selections (for G = 1 this is the reference's per-head selection).
+#include <atomic>
+
 #include "ekv_common.h"
 #include "gaussian_device.h"
 #include "../../include/entmaxkv.h"
@@ -311,6 +313,12 @@ extern "C" int ekv_gaussian_moments(
   a.sigma_p = sigma_p;
   a.partials = (float4*)workspace;
   a.seq_lens = seq_lens;
+  {
+    // consecutive launches scan in opposite orders (the reason is the
+    // criticality scan's, next_scan_order)
+    static std::atomic<unsigned> scans{0};
+    a.rev = (int)(scans.fetch_add(1, std::memory_order_relaxed) & 1u);
+  }
   hipStream_t s = (hipStream_t)stream;
   return dispatch_dtype(dtype, [&](auto tv) {
     using T = decltype(tv);

@@ -268,6 +268,7 @@ static int topk_step(
   t.key_cap = num_pages;
   t.seq_lens = seq_lens;
   t.prescored = 0;
+  t.scan_rev = topk::next_scan_order();
   if (app) {
     t.app_k = app->k_new;
     t.app_v = app->v_new;
@@ -285,7 +286,7 @@ static int topk_step(
     const int rc = topk::criticality_split_scores(
         q, q_stride_b, q_stride_h, kmin, kmax, s_stride_b, s_stride_h, s_stride_page,
         alibi_slopes, scores, B, H, Hkv, D, num_pages, page_size, seq_len, q_pos, nullptr, dtype,
-        s);
+        s, t.scan_rev);
     if (rc) return rc;
     t.prescored = 1;
   }

@@ -3,6 +3,8 @@
 // criticality launches and the fused top-k decode launch.
 #pragma once
 
+#include <atomic>
+
 #include "ekv_common.h"
 
 // Phase timestamps (experiment builds define EKV_CSTAMP before including).
@@ -29,15 +31,29 @@ constexpr int kMaxStagedKeys = 16384;
 // histograms; 37 KB at fp32 and G = 8): the dynamic LDS sizing leaves it free.
 constexpr int kSelectStaticLds = 40960;
 
+// Consecutive criticality scans read the bounds in opposite orders (returns 0
+// or 1 alternately, over the whole process), so that a step starts with the
+// pages the last one read most recently: the GPU's memory-side cache (256 MB)
+// holds the tail of the last step's 268 MB at the headline shape, and an
+// unchanged order would evict each line just before it is read again.  Every
+// result is the same in either order (each page's score and key is computed
+// alone; the key histogram is an integer count).  A launch captured in a
+// graph keeps the order of its capture.
+inline int next_scan_order() {
+  static std::atomic<unsigned> scans{0};
+  return (int)(scans.fetch_add(1, std::memory_order_relaxed) & 1u);
+}
+
 // Host launcher (criticality_topk.hip) of the criticality scores alone over
 // many workgroups per (b, kv head), whatever the head count: the fused top-k
-// step runs it first when one workgroup per head would leave CUs idle.
+// step runs it first when one workgroup per head would leave CUs idle.  `rev`
+// reverses the order in which its workgroups take their pages.
 int criticality_split_scores(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                              const void* kmin, const void* kmax, int64_t s_stride_b,
                              int64_t s_stride_h, int64_t s_stride_page,
                              const float* alibi_slopes, void* scores, int B, int H, int Hkv,
                              int D, int num_pages, int page_size, int seq_len, int q_pos,
-                             const int32_t* seq_lens, int dtype, hipStream_t s);
+                             const int32_t* seq_lens, int dtype, hipStream_t s, int rev = 0);
 
 // Top-k geometry of batch element b.  With per-sequence lengths, sequence b
 // scores its pages [0, P_b - 1) (the partial last page excluded), selects
@@ -794,7 +810,7 @@ __device__ __forceinline__ T* criticality_scan_head(
     const T* __restrict__ kmax, int64_t ssb, int64_t ssh, int64_t ssp,
     const float* __restrict__ slopes, T* __restrict__ scores, int H, int stride, int num_pages,
     int page_size, int seq_len, int q_pos, int b, int kvh, uint32_t* lds_keys,
-    unsigned* hist0 = nullptr, int* lds_next = nullptr) {
+    unsigned* hist0 = nullptr, int* lds_next = nullptr, bool rev = false) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int SEGS = NT / LPR;
   constexpr int ROUND = SEGS * U;
@@ -867,10 +883,12 @@ __device__ __forceinline__ T* criticality_scan_head(
       if (lane == 0) v = atomicAdd(lds_next, 1);
       return __builtin_amdgcn_readfirstlane(v);
     };
+    // rev: the chunks are handed out last first
+    const int nch = (num_pages + CHUNK - 1) / CHUNK;
     int c = grab();
-    while (c * CHUNK < num_pages) {
+    while (c < nch) {
       const int c_next = grab();
-      body(c * CHUNK, WSEG, seg % WSEG);
+      body((rev ? nch - 1 - c : c) * CHUNK, WSEG, seg % WSEG);
       c = c_next;
     }
   } else {
