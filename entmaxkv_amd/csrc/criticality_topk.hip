@@ -81,7 +81,7 @@ __global__ __launch_bounds__(kThreads) void criticality_kernel(
     const T* __restrict__ kmax, int64_t ssb, int64_t ssh, int64_t ssp,
     const float* __restrict__ slopes, T* __restrict__ scores, int H, int Hkv, int stride,
     int page_size, int seq_len_all, int q_pos_all, const int32_t* __restrict__ seq_lens,
-    int rev) {
+    int rev, int nt) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int SEGS = kThreads / LPR;
   // rev: the workgroups take their (b, kv head, page round) in the opposite
@@ -113,8 +113,8 @@ __global__ __launch_bounds__(kThreads) void criticality_kernel(
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int p = min(p_base + u * SEGS, num_pages - 1);
-    lo[u] = ld16(kmn + (int64_t)p * ssp + col);
-    hi[u] = ld16(kmx + (int64_t)p * ssp + col);
+    lo[u] = ld16_sel(kmn + (int64_t)p * ssp + col, nt);
+    hi[u] = ld16_sel(kmx + (int64_t)p * ssp + col, nt);
   }
   T* sbase = scores + ((int64_t)b * H + h0) * stride;
 #pragma unroll
@@ -249,7 +249,8 @@ extern "C" int ekv_page_criticality(const void* q, int64_t q_stride_b, int64_t q
         hipLaunchKernelGGL((criticality_kernel<T, LPR, G>), grid, dim3(kThreads), 0, s, (const T*)q,
                            q_stride_b, q_stride_h, (const T*)kmin, (const T*)kmax, s_stride_b,
                            s_stride_h, s_stride_page, alibi_slopes, (T*)scores, H, Hkv, num_pages,
-                           page_size, seq_len, q_pos, seq_lens, next_scan_order());
+                           page_size, seq_len, q_pos, seq_lens, next_scan_order(),
+                           stream_nt(B, Hkv, num_pages, D, dtype));
         if (k_select >= 0) {
           int rc = check_launch("criticality_kernel");
           if (rc) return rc;
@@ -274,7 +275,8 @@ int criticality_split_scores(const void* q, int64_t q_stride_b, int64_t q_stride
                              int64_t s_stride_h, int64_t s_stride_page,
                              const float* alibi_slopes, void* scores, int B, int H, int Hkv,
                              int D, int num_pages, int page_size, int seq_len, int q_pos,
-                             const int32_t* seq_lens, int dtype, hipStream_t s, int rev) {
+                             const int32_t* seq_lens, int dtype, hipStream_t s, int rev,
+                             int nt) {
   return dispatch_dtype(dtype, [&](auto tv) {
     using T = decltype(tv);
     return dispatch_lpr<T>(D, [&](auto lpr) {
@@ -287,7 +289,7 @@ int criticality_split_scores(const void* q, int64_t q_stride_b, int64_t q_stride
                            (const T*)q, q_stride_b, q_stride_h, (const T*)kmin,
                            (const T*)kmax, s_stride_b, s_stride_h, s_stride_page, alibi_slopes,
                            (T*)scores, H, Hkv, num_pages, page_size, seq_len, q_pos, seq_lens,
-                           rev);
+                           rev, nt);
         return check_launch("criticality_kernel");
       });
     });

@@ -1142,6 +1142,7 @@ struct SelectArgs {
   int app_pos = -1;
   const int32_t* seq_lens;  // [B] per-sequence lengths (ragged batch) or null
   int scan_rev = 0;         // the scan hands out its page chunks last first
+  int scan_nt = 0;          // the scan's loads are non-temporal (stream_nt)
 };
 
 // One (b, kv head) per workgroup end to end: criticality scan of every page
@@ -1209,7 +1210,8 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
         (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
         a.slopes, (T*)t.scores, a.H, t.num_pages, r.count, a.page_size, r.seq_len, r.q_pos, b,
         kvh, G == 1 ? (keep ? keys : nullptr) : head_keys,
-        G == 1 && keep ? &sel_hist[0][0] : nullptr, &scan_next, t.scan_rev != 0);
+        G == 1 && keep ? &sel_hist[0][0] : nullptr, &scan_next, t.scan_rev != 0,
+        t.scan_nt != 0);
   } else if (G > 1 && head_keys &&
              (t.num_pages * (int)sizeof(T)) % 16 == 0 && ((uintptr_t)sbase & 15) == 0) {
     // every query head's keys into LDS once (the select reads them per pass):

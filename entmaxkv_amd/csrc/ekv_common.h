@@ -82,6 +82,16 @@ template <typename T> struct VecRaw {
   static constexpr int N = 16 / sizeof(T);
   uint4 raw;
   __device__ __forceinline__ void load(const T* p) { raw = *reinterpret_cast<const uint4*>(p); }
+  // non-temporal when nt (see ld16_nt)
+  __device__ __forceinline__ void load_sel(const T* p, bool nt) {
+    if (nt) {
+      typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+      const u4 v = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
+      raw = make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+      raw = *reinterpret_cast<const uint4*>(p);
+    }
+  }
   __device__ __forceinline__ float get(int i) const {
     return to_f<T>(reinterpret_cast<const T*>(&raw)[i]);
   }
@@ -152,6 +162,31 @@ __device__ __forceinline__ uint4 bit_select(const uint4& a, const uint4& b, cons
 }
 
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+// A non-temporal 16-byte load (`nt`): for data streamed once per step (the
+// page statistics of the scans), so that it does not push out of the caches
+// what the step reads again (K and V rows).
+__device__ __forceinline__ uint4 ld16_nt(const void* p) {
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  const u4 v = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 ld16_sel(const void* p, bool nt) {
+  return nt ? ld16_nt(p) : ld16(p);
+}
+
+// Statistics scans stream their bounds / moments with non-temporal loads when
+// they read more than this per launch: beyond it they cannot stay in the
+// GPU's 256 MB memory-side cache from one step to the next anyway, and
+// normal loads would push out the K and V rows that the next step reads
+// again; below it (128 MiB at B4 H32 L32k) normal loads keep them cached.
+constexpr int64_t kStreamNtBytes = 160ll << 20;
+
+// Whether a scan of two [B, Hkv, pages, D] statistics of storage dtype code
+// `dtype` (0 fp32, 1 fp16, 2 bf16) streams with non-temporal loads.
+inline bool stream_nt(int B, int Hkv, int pages, int D, int dtype) {
+  const int64_t esize = dtype == 0 ? 4 : 2;
+  return (int64_t)B * Hkv * pages * D * esize * 2 > kStreamNtBytes;
+}
 
 // ---------------------------------------------------------------------------
 // wave-level reductions (wave64)

@@ -216,6 +216,8 @@ struct MomentsArgs {
   float4* partials;     // [B, H, splits] (Sum mu, Sum mu^2, Sum var, 0)
   const int32_t* seq_lens;  // [B] per-sequence lengths (ragged batch) or null
   int rev = 0;              // LDS-staged scans take their rounds last first
+  int nt = 0;               // non-temporal loads (kStreamNtBytes; a template
+                            // parameter of the launch)
 };
 
 // Moments of pages [split * pages_per_split, ...) of one (b, kv head) for its
@@ -231,7 +233,7 @@ struct MomentsArgs {
 // to launch (a.rev) like the criticality scan's.
 constexpr int kMomentLdsEntries = 4096;
 
-template <typename T, int LPR, int G, int NT, int U, bool kLdsOut = false>
+template <typename T, int LPR, int G, int NT, int U, bool kLdsOut = false, bool kNt = false>
 __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int b, int kvh,
                                                       int split) {
   constexpr int VEC = 16 / sizeof(T);
@@ -289,8 +291,8 @@ __device__ __forceinline__ void moments_partial_block(const MomentsArgs& a, int 
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int p = min(p0 + u * SEGS + seg, p_end - 1);
-      mv[u].load(km + (int64_t)p * a.ssp + col);
-      sv[u].load(ks + (int64_t)p * a.ssp + col);
+      mv[u].load_sel(km + (int64_t)p * a.ssp + col, kNt);
+      sv[u].load_sel(ks + (int64_t)p * a.ssp + col, kNt);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the arithmetic
   };

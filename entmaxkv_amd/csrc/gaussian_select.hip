@@ -35,15 +35,15 @@ constexpr int kThreads = 256;
 // slightly faster than two and four at the headline shape
 constexpr int kMomentUnroll = 1;
 
-template <typename T, int LPR, int G>
+template <typename T, int LPR, int G, bool kNt>
 __global__ __launch_bounds__(moment_threads(G)) void moments_kernel(MomentsArgs a) {
   const int bkv = blockIdx.y;
   if (a.pages_per_split * G <= kMomentLdsEntries)
-    moments_partial_block<T, LPR, G, moment_threads(G), kMomentUnroll, true>(a, bkv / a.Hkv,
-                                                                           bkv % a.Hkv, blockIdx.x);
+    moments_partial_block<T, LPR, G, moment_threads(G), kMomentUnroll, true, kNt>(
+        a, bkv / a.Hkv, bkv % a.Hkv, blockIdx.x);
   else
-    moments_partial_block<T, LPR, G, moment_threads(G), kMomentUnroll>(a, bkv / a.Hkv,
-                                                                     bkv % a.Hkv, blockIdx.x);
+    moments_partial_block<T, LPR, G, moment_threads(G), kMomentUnroll, false, kNt>(
+        a, bkv / a.Hkv, bkv % a.Hkv, blockIdx.x);
 }
 
 // One wave per (b, h): global moments from the partials (reduced by the
@@ -319,6 +319,7 @@ extern "C" int ekv_gaussian_moments(
     static std::atomic<unsigned> scans{0};
     a.rev = (int)(scans.fetch_add(1, std::memory_order_relaxed) & 1u);
   }
+  a.nt = stream_nt(B, Hkv, pages_for_stats, D, dtype) ? 1 : 0;
   hipStream_t s = (hipStream_t)stream;
   return dispatch_dtype(dtype, [&](auto tv) {
     using T = decltype(tv);
@@ -326,8 +327,12 @@ extern "C" int ekv_gaussian_moments(
       constexpr int LPR = decltype(lpr)::value;
       return dispatch_group(H / Hkv, [&](auto gv) {
         constexpr int G = decltype(gv)::value;
-        hipLaunchKernelGGL((moments_kernel<T, LPR, G>), dim3(a.splits, B * Hkv),
-                           dim3(moment_threads(G)), 0, s, a);
+        if (a.nt)
+          hipLaunchKernelGGL((moments_kernel<T, LPR, G, true>), dim3(a.splits, B * Hkv),
+                             dim3(moment_threads(G)), 0, s, a);
+        else
+          hipLaunchKernelGGL((moments_kernel<T, LPR, G, false>), dim3(a.splits, B * Hkv),
+                             dim3(moment_threads(G)), 0, s, a);
         return check_launch("moments_kernel");
       });
     });

@@ -269,6 +269,7 @@ static int topk_step(
   t.seq_lens = seq_lens;
   t.prescored = 0;
   t.scan_rev = topk::next_scan_order();
+  t.scan_nt = stream_nt(B, Hkv, num_pages, D, dtype) ? 1 : 0;
   if (app) {
     t.app_k = app->k_new;
     t.app_v = app->v_new;
@@ -286,7 +287,7 @@ static int topk_step(
     const int rc = topk::criticality_split_scores(
         q, q_stride_b, q_stride_h, kmin, kmax, s_stride_b, s_stride_h, s_stride_page,
         alibi_slopes, scores, B, H, Hkv, D, num_pages, page_size, seq_len, q_pos, nullptr, dtype,
-        s, t.scan_rev);
+        s, t.scan_rev, t.scan_nt);
     if (rc) return rc;
     t.prescored = 1;
   }

@@ -47,13 +47,15 @@ inline int next_scan_order() {
 // Host launcher (criticality_topk.hip) of the criticality scores alone over
 // many workgroups per (b, kv head), whatever the head count: the fused top-k
 // step runs it first when one workgroup per head would leave CUs idle.  `rev`
-// reverses the order in which its workgroups take their pages.
+// reverses the order in which its workgroups take their pages; `nt` makes its
+// loads non-temporal (kStreamNtBytes).
 int criticality_split_scores(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                              const void* kmin, const void* kmax, int64_t s_stride_b,
                              int64_t s_stride_h, int64_t s_stride_page,
                              const float* alibi_slopes, void* scores, int B, int H, int Hkv,
                              int D, int num_pages, int page_size, int seq_len, int q_pos,
-                             const int32_t* seq_lens, int dtype, hipStream_t s, int rev = 0);
+                             const int32_t* seq_lens, int dtype, hipStream_t s, int rev = 0,
+                             int nt = 0);
 
 // Top-k geometry of batch element b.  With per-sequence lengths, sequence b
 // scores its pages [0, P_b - 1) (the partial last page excluded), selects
@@ -810,7 +812,7 @@ __device__ __forceinline__ T* criticality_scan_head(
     const T* __restrict__ kmax, int64_t ssb, int64_t ssh, int64_t ssp,
     const float* __restrict__ slopes, T* __restrict__ scores, int H, int stride, int num_pages,
     int page_size, int seq_len, int q_pos, int b, int kvh, uint32_t* lds_keys,
-    unsigned* hist0 = nullptr, int* lds_next = nullptr, bool rev = false) {
+    unsigned* hist0 = nullptr, int* lds_next = nullptr, bool rev = false, bool nt = false) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int SEGS = NT / LPR;
   constexpr int ROUND = SEGS * U;
@@ -841,8 +843,8 @@ __device__ __forceinline__ T* criticality_scan_head(
     for (int u = 0; u < U; ++u) {
       const int p = base + u * step + off;
       if (p < num_pages) {
-        lo[u] = ld16(kmn + (int64_t)p * ssp + col);
-        hi[u] = ld16(kmx + (int64_t)p * ssp + col);
+        lo[u] = ld16_sel(kmn + (int64_t)p * ssp + col, nt);
+        hi[u] = ld16_sel(kmx + (int64_t)p * ssp + col, nt);
       }
     }
 #pragma unroll
