@@ -1143,13 +1143,28 @@ struct SelectArgs {
   const int32_t* seq_lens;  // [B] per-sequence lengths (ragged batch) or null
   int scan_rev = 0;         // the scan hands out its page chunks last first
   int scan_nt = 0;          // the scan's loads are non-temporal (stream_nt)
+  // the paired launch (G == 1, fewer (b, kv head) pairs than CUs): two
+  // workgroups per (b, kv head), each scanning half of the pages, with one
+  // arrival word per pair (any value on entry that is not pair_tag; left 0)
+  unsigned long long* pair_cnt = nullptr;
+  unsigned long long pair_tag = 0;
 };
 
 // One (b, kv head) per workgroup end to end: criticality scan of every page
 // (or, when t.prescored, the scores a split scan over every CU wrote), top-k
 // (page table to global memory and to LDS), then phases 1-3 of the decode on
 // the selected pages.  Keys and then scores share the dynamic LDS.
-template <typename T, int LPR, int G, int UC, int UD>
+//
+// kPair (G == 1): two workgroups per (b, kv head) scan one half of its pages
+// each, storing their scores with store_through, and count their arrival by
+// exchanging t.pair_tag into the pair's word (a fresh tag per launch, so a
+// stale word never matches, and the second to arrive sets it back to zero,
+// so a replayed graph with the same tag starts clean).  The first to arrive
+// leaves; the second loads its partner's half of the scores with
+// load_through, adds their keys to its LDS keys and first-digit histogram, and
+// selects and decodes as a lone workgroup would.  The scores of every page are
+// computed alone, so the results are those of the one-workgroup launch.
+template <typename T, int LPR, int G, int UC, int UD, bool kPair = false>
 __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a, SelectArgs t) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int D = LPR * VEC;
@@ -1168,7 +1183,9 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
   HeadShared sh{hist, part, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
   sh.wmax = wmax;
 
-  const int bkv = blockIdx.x;
+  static_assert(!kPair || G == 1, "the paired launch is for single-head groups");
+  const int bkv = kPair ? blockIdx.x >> 1 : blockIdx.x;
+  const int pair_half = kPair ? blockIdx.x & 1 : 0;
   const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
   uint32_t* keys = reinterpret_cast<uint32_t*>(stage);
   // the scan's chunk counter (and, G == 1, the select's histograms) start at zero
@@ -1205,7 +1222,21 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
   uint32_t* head_keys = G > 1 && t.head_keys ? list + t.list_words : nullptr;
   EKV_STAMP(0);
   const T* sbase = (const T*)t.scores + ((int64_t)b * a.H + kvh * G) * t.num_pages;
-  if (!t.prescored) {
+  // kPair: this workgroup's half of the pages [pp0, pp1) (split on a chunk)
+  int pp0 = 0, pp1 = r.count;
+  if constexpr (kPair) {
+    constexpr int kChunk = UC * (64 / LPR);
+    const int mid = min(r.count, (r.count / 2 + kChunk - 1) / kChunk * kChunk);
+    if (pair_half) pp0 = mid;
+    else pp1 = mid;
+  }
+  if (kPair) {
+    topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC, true, true>(
+        (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
+        a.slopes, (T*)t.scores, a.H, t.num_pages, pp1, a.page_size, r.seq_len, r.q_pos, b, kvh,
+        keys, &sel_hist[0][0], &scan_next, t.scan_rev != 0, t.scan_nt != 0, pp0);
+    __builtin_amdgcn_s_waitcnt(0);  // the stores through are complete
+  } else if (!t.prescored) {
     topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC, true>(
         (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
         a.slopes, (T*)t.scores, a.H, t.num_pages, r.count, a.page_size, r.seq_len, r.q_pos, b,
@@ -1258,10 +1289,30 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
     }
   }
   __syncthreads();
+  if constexpr (kPair) {
+    if (threadIdx.x == 0) {
+      const unsigned long long old = __hip_atomic_exchange(
+          t.pair_cnt + bkv, t.pair_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool second = old == t.pair_tag;
+      if (second)
+        __hip_atomic_store(t.pair_cnt + bkv, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      scan_next = second ? 1 : 0;
+    }
+    __syncthreads();
+    if (scan_next == 0) return;  // the partner selects and decodes
+    // the partner's half: its scores, their keys and first-digit counts
+    const int q0 = pair_half ? 0 : pp1, q1 = pair_half ? pp0 : r.count;
+    for (int p = q0 + (int)threadIdx.x; p < q1; p += kHeadThreads) {
+      const uint32_t key = topk::ScoreKey<T>::key(topk::load_through(sbase + p));
+      keys[p] = key;
+      atomicAdd(&sel_hist[0][key >> (topk::ScoreKey<T>::kBits - 8)], 1u);
+    }
+    __syncthreads();
+  }
   EKV_STAMP(1);
   int32_t* pi = const_cast<int32_t*>(a.page_indices) + b * a.pisb + kvh * a.pish;
   // G == 1: the scan left the keys in LDS; prescored, the select stages them
-  const bool staged = keep && !t.prescored;
+  const bool staged = kPair || (keep && !t.prescored);
   // the page table goes to LDS only here and to global memory at the end, so
   // that no barrier of the select or the decode waits on its stores
   topk::topk_select_block<T, G, kHeadThreads>(

@@ -2,6 +2,8 @@
 // decode step and the fused Gaussian select + decode step.  The kernels and
 // their per-(dtype, group) launchers live in decode_device.h /
 // decode_launch.h; decode_inst.hip instantiates them.
+#include <atomic>
+
 #include "decode_device.h"
 #include "../../include/entmaxkv.h"
 
@@ -283,7 +285,16 @@ static int topk_step(
   // fewer (b, kv head) pairs than CUs: the criticality scan, the step's
   // largest part, runs over every CU in a launch of its own, and the fused
   // launch starts from its scores
-  if (B * Hkv < device_cus()) {
+  if (G == 1 && 2 * B * Hkv <= device_cus() && max_tokens >= 2 &&
+      ((uintptr_t)workspace & 7) == 0) {
+    // two workgroups per (b, kv head) share its scan inside the one launch;
+    // their arrival words are the first B * Hkv 8-byte words of the
+    // workspace, whose scores this launch does not use
+    static std::atomic<unsigned long long> launches{0};
+    t.pair_cnt = (unsigned long long*)workspace;
+    t.pair_tag = ((launches.fetch_add(1, std::memory_order_relaxed) + 1) *
+                  0x9E3779B97F4A7C15ull) | 1ull;
+  } else if (B * Hkv < device_cus()) {
     const int rc = topk::criticality_split_scores(
         q, q_stride_b, q_stride_h, kmin, kmax, s_stride_b, s_stride_h, s_stride_page,
         alibi_slopes, scores, B, H, Hkv, D, num_pages, page_size, seq_len, q_pos, nullptr, dtype,

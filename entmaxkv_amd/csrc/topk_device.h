@@ -797,6 +797,31 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
   EKV_CSTAMP(4);
 }
 
+// Agent-scope (write-through) store and load of one storage element: a store
+// reaches the level every XCD reads before the wave's waitcnt returns, and a
+// load is served from there, so two workgroups on different XCDs can hand
+// data over without a fence (see the paired top-k launch).
+template <typename T>
+__device__ __forceinline__ void store_through(T* p, T v) {
+  if constexpr (sizeof(T) == 4) {
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    __hip_atomic_store(reinterpret_cast<uint16_t*>(p), __builtin_bit_cast(uint16_t, v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+template <typename T>
+__device__ __forceinline__ T load_through(const T* p) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p),
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  } else {
+    return __builtin_bit_cast(T, __hip_atomic_load(reinterpret_cast<const uint16_t*>(p),
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  }
+}
+
 // Criticality scan of one (b, kv head) by a workgroup of NT threads: scores
 // of the G query heads for pages [0, count) written to `scores`
 // ([B, H, stride], query dtype; count <= stride) and, when `lds_keys` is
@@ -805,14 +830,17 @@ __device__ __forceinline__ void topk_select_block(const T* __restrict__ s0, int6
 // zero and visible on entry) every key's top 8 bits are counted there too.  A
 // row segment of LPR lanes owns one page and loads its min and max rows with
 // 16-byte loads, U pages per segment in flight.  Returns the head's score
-// base pointer.
-template <typename T, int LPR, int G, int NT, int U, bool kChunked = false>
+// base pointer.  Chunked, the scan covers pages [p_begin, num_pages) only,
+// and kThrough stores the scores with store_through.
+template <typename T, int LPR, int G, int NT, int U, bool kChunked = false,
+          bool kThrough = false>
 __device__ __forceinline__ T* criticality_scan_head(
     const T* __restrict__ q, int64_t qsb, int64_t qsh, const T* __restrict__ kmin,
     const T* __restrict__ kmax, int64_t ssb, int64_t ssh, int64_t ssp,
     const float* __restrict__ slopes, T* __restrict__ scores, int H, int stride, int num_pages,
     int page_size, int seq_len, int q_pos, int b, int kvh, uint32_t* lds_keys,
-    unsigned* hist0 = nullptr, int* lds_next = nullptr, bool rev = false, bool nt = false) {
+    unsigned* hist0 = nullptr, int* lds_next = nullptr, bool rev = false, bool nt = false,
+    int p_begin = 0) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int SEGS = NT / LPR;
   constexpr int ROUND = SEGS * U;
@@ -862,7 +890,8 @@ __device__ __forceinline__ T* criticality_scan_head(
         const T sv = from_f<T>(acc);
         key = ScoreKey<T>::key(sv);
         if (p < num_pages && sl == 0) {
-          sbase[(int64_t)g * stride + p] = sv;
+          if constexpr (kThrough) store_through(sbase + (int64_t)g * stride + p, sv);
+          else sbase[(int64_t)g * stride + p] = sv;
           if (G > 1 && keep_keys) lds_keys[g * stride + p] = key;
         }
       }
@@ -886,11 +915,11 @@ __device__ __forceinline__ T* criticality_scan_head(
       return __builtin_amdgcn_readfirstlane(v);
     };
     // rev: the chunks are handed out last first
-    const int nch = (num_pages + CHUNK - 1) / CHUNK;
+    const int nch = (num_pages - p_begin + CHUNK - 1) / CHUNK;
     int c = grab();
     while (c < nch) {
       const int c_next = grab();
-      body((rev ? nch - 1 - c : c) * CHUNK, WSEG, seg % WSEG);
+      body(p_begin + (rev ? nch - 1 - c : c) * CHUNK, WSEG, seg % WSEG);
       c = c_next;
     }
   } else {

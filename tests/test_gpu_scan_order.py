@@ -3,8 +3,8 @@ next (consecutive decode steps then start with the pages the last one read
 most recently, which the GPU's memory-side cache still holds).  The order must
 not change any result: two consecutive launches on the same inputs, which run
 in opposite orders, give the same bits.  Shapes cover the fused scan (B * Hkv
-= 256), the prescored scan launch (128), G = 1 and G = 4, and moment scans
-whose last round is partial.
+= 256), the paired launch (128, G = 1), the prescored scan launch (128,
+G = 4), and moment scans whose last round is partial.
 """
 
 from __future__ import annotations
@@ -68,6 +68,41 @@ def test_topk_step_same_bits_in_both_orders(B, Hkv, G, dtype):
                                       niter=2, append_cache=False)
         torch.cuda.synchronize()
         got.append((out, cache._page_indices_buf.clone()))
+    for out, table in got[1:]:
+        _equal(got[0][0], out, "out")
+        _equal(got[0][1], table, "page table")
+
+
+@pytest.mark.parametrize("fill", ["random", "ones"])
+def test_paired_topk_any_workspace(fill):
+    """B * Hkv = 128 with single-head groups runs the paired launch (two
+    workgroups per (b, kv head) scanning half of its pages each); its arrival
+    words live in the decode workspace, which a caller need not initialise.
+    Random bytes, or every byte 0xff, in the workspace between steps leave
+    the results unchanged."""
+    from entmaxkv_amd import PagedKVCache, sparse_attention_decode_paged
+    _case(test="paired_workspace", fill=fill)
+    dtype = "fp16"
+    rng = np.random.default_rng(820)
+    B, Hkv, S, D, budget = 4, 32, 16 * 200 + 9, 128, 1024
+    k = randn(rng, (B, Hkv, S, D), dtype)
+    v = randn(rng, (B, Hkv, S, D), dtype)
+    q = to_dev(randn(rng, (B, Hkv, 1, D), dtype), dtype)
+    cache = PagedKVCache(page_size=16)
+    cache.initialize(to_dev(k, dtype), to_dev(v, dtype))
+    got = []
+    for step in range(3):
+        for ws in cache._paged_decode_workspaces.values():
+            if fill == "random":
+                ws.buf.copy_(torch.randint(0, 256, ws.buf.shape, dtype=torch.uint8))
+            else:
+                ws.buf.fill_(255)
+        out = torch.zeros(B, Hkv, 1, D, dtype=TORCH_DT[dtype], device="cuda")
+        sparse_attention_decode_paged(q, cache, None, None, out, budget, None, None, alpha=1.5,
+                                      niter=2, append_cache=False)
+        torch.cuda.synchronize()
+        got.append((out, cache._page_indices_buf.clone()))
+    assert torch.isfinite(got[0][0].float()).all()
     for out, table in got[1:]:
         _equal(got[0][0], out, "out")
         _equal(got[0][1], table, "page table")
