@@ -1143,7 +1143,7 @@ struct SelectArgs {
   const int32_t* seq_lens;  // [B] per-sequence lengths (ragged batch) or null
   int scan_rev = 0;         // the scan hands out its page chunks last first
   int scan_nt = 0;          // the scan's loads are non-temporal (stream_nt)
-  // the paired launch (G == 1, fewer (b, kv head) pairs than CUs): two
+  // the paired launch (2 B Hkv <= CUs, G <= 2, every head's keys in LDS): two
   // workgroups per (b, kv head), each scanning half of the pages, with one
   // arrival word per pair (any value on entry that is not pair_tag; left 0)
   unsigned long long* pair_cnt = nullptr;
@@ -1155,14 +1155,15 @@ struct SelectArgs {
 // (page table to global memory and to LDS), then phases 1-3 of the decode on
 // the selected pages.  Keys and then scores share the dynamic LDS.
 //
-// kPair (G == 1): two workgroups per (b, kv head) scan one half of its pages
+// kPair: two workgroups per (b, kv head) scan one half of its pages
 // each, storing their scores with store_through, and count their arrival by
 // exchanging t.pair_tag into the pair's word (a fresh tag per launch, so a
 // stale word never matches, and the second to arrive sets it back to zero,
 // so a replayed graph with the same tag starts clean).  The first to arrive
 // leaves; the second loads its partner's half of the scores with
-// load_through, adds their keys to its LDS keys and first-digit histogram, and
-// selects and decodes as a lone workgroup would.  The scores of every page are
+// load_through, adds their keys to its LDS keys (G == 1: and first-digit
+// histogram; G > 1: every query head's keys, which the launch must keep in
+// LDS), and selects and decodes as a lone workgroup would.  The scores of every page are
 // computed alone, so the results are those of the one-workgroup launch.
 template <typename T, int LPR, int G, int UC, int UD, bool kPair = false>
 __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a, SelectArgs t) {
@@ -1183,7 +1184,6 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
   HeadShared sh{hist, part, s_tau, sup_row, sup_p, flag_cnt, red, s_pages};
   sh.wmax = wmax;
 
-  static_assert(!kPair || G == 1, "the paired launch is for single-head groups");
   const int bkv = kPair ? blockIdx.x >> 1 : blockIdx.x;
   const int pair_half = kPair ? blockIdx.x & 1 : 0;
   const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
@@ -1234,7 +1234,8 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
     topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC, true, true>(
         (const T*)a.q, a.qsb, a.qsh, (const T*)t.kmin, (const T*)t.kmax, t.ssb, t.ssh, t.ssp,
         a.slopes, (T*)t.scores, a.H, t.num_pages, pp1, a.page_size, r.seq_len, r.q_pos, b, kvh,
-        keys, &sel_hist[0][0], &scan_next, t.scan_rev != 0, t.scan_nt != 0, pp0);
+        G == 1 ? keys : head_keys, G == 1 ? &sel_hist[0][0] : nullptr, &scan_next,
+        t.scan_rev != 0, t.scan_nt != 0, pp0);
     __builtin_amdgcn_s_waitcnt(0);  // the stores through are complete
   } else if (!t.prescored) {
     topk::criticality_scan_head<T, LPR, G, kHeadThreads, UC, true>(
@@ -1300,12 +1301,22 @@ __global__ __launch_bounds__(kHeadThreads) void topk_decode_kernel(DecodeArgs a,
     }
     __syncthreads();
     if (scan_next == 0) return;  // the partner selects and decodes
-    // the partner's half: its scores, their keys and first-digit counts
+    // the partner's half: its scores' keys (G == 1: and first-digit counts;
+    // G > 1: every query head's keys)
     const int q0 = pair_half ? 0 : pp1, q1 = pair_half ? pp0 : r.count;
-    for (int p = q0 + (int)threadIdx.x; p < q1; p += kHeadThreads) {
-      const uint32_t key = topk::ScoreKey<T>::key(topk::load_through(sbase + p));
-      keys[p] = key;
-      atomicAdd(&sel_hist[0][key >> (topk::ScoreKey<T>::kBits - 8)], 1u);
+    if constexpr (G == 1) {
+      for (int p = q0 + (int)threadIdx.x; p < q1; p += kHeadThreads) {
+        const uint32_t key = topk::ScoreKey<T>::key(topk::load_through(sbase + p));
+        keys[p] = key;
+        atomicAdd(&sel_hist[0][key >> (topk::ScoreKey<T>::kBits - 8)], 1u);
+      }
+    } else {
+      const int w = q1 - q0;
+      for (int i = (int)threadIdx.x; i < G * w; i += kHeadThreads) {
+        const int g = i / w, p = q0 + i % w;
+        head_keys[g * t.num_pages + p] =
+            topk::ScoreKey<T>::key(topk::load_through(sbase + (int64_t)g * t.num_pages + p));
+      }
     }
     __syncthreads();
   }

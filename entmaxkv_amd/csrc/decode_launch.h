@@ -65,13 +65,9 @@ int Launch<T, G>::topk(DecodeArgs a, SelectArgs t, int B, int Hkv, int D, int to
     // queue up); the G query heads of a group share every page load
     constexpr int UC = G >= 8 ? 1 : (G == 1 ? 2 : 8 / G);
     constexpr int UD = G >= 4 ? 2 : 8 / G;
-    // the paired launch (G == 1 only) or the one-workgroup launch
-    auto kern = topk_decode_kernel<T, LPR, G, UC, UD>;
-    if constexpr (G == 1) {
-      if (t.pair_cnt) kern = topk_decode_kernel<T, LPR, G, UC, UD, true>;
-    } else {
-      if (t.pair_cnt) return EKV_OK;  // not for groups: the caller falls back
-    }
+    // the paired launch or the one-workgroup launch
+    auto kern = t.pair_cnt ? topk_decode_kernel<T, LPR, G, UC, UD, true>
+                           : topk_decode_kernel<T, LPR, G, UC, UD>;
     const int64_t avail = lds_left((const void*)kern, "topk_decode_kernel");
     if (avail < 0) return EKV_ERR_HIP;
     // keys (G == 1), or page ranks + candidate lists (all G at once when they
@@ -101,6 +97,8 @@ int Launch<T, G>::topk(DecodeArgs a, SelectArgs t, int B, int Hkv, int D, int to
       }
     }
     if (lds < 0 || lds > avail) return EKV_OK;  // too big: the caller falls back
+    // the paired launch of groups hands every query head's keys over in LDS
+    if (G > 1 && t.pair_cnt && !t.head_keys) return EKV_OK;
     const int rc = set_dynamic_lds((const void*)kern, (size_t)lds, "topk_decode_kernel");
     if (rc) return rc;
     hipLaunchKernelGGL(kern, dim3(B * Hkv * (t.pair_cnt ? 2 : 1)), dim3(kHeadThreads),

@@ -285,11 +285,12 @@ static int topk_step(
   // fewer (b, kv head) pairs than CUs: the criticality scan, the step's
   // largest part, runs over every CU in a launch of its own, and the fused
   // launch starts from its scores
-  if (G == 1 && 2 * B * Hkv <= device_cus() && max_tokens >= 2 &&
+  if (G <= 2 && 2 * B * Hkv <= device_cus() && max_tokens >= 2 &&
       ((uintptr_t)workspace & 7) == 0) {
     // two workgroups per (b, kv head) share its scan inside the one launch;
     // their arrival words are the first B * Hkv 8-byte words of the
-    // workspace, whose scores this launch does not use
+    // workspace, whose scores this launch does not use.  (Groups of 4 and 8
+    // measured slower paired: config 4 102.9 against 108.6 us.)
     static std::atomic<unsigned long long> launches{0};
     t.pair_cnt = (unsigned long long*)workspace;
     t.pair_tag = ((launches.fetch_add(1, std::memory_order_relaxed) + 1) *
@@ -303,13 +304,28 @@ static int topk_step(
     t.prescored = 1;
   }
   int handled = 0;
-  const int rc = dispatch_dtype(dtype, [&](auto tv) {
-    using T = decltype(tv);
-    return dispatch_group(G, [&](auto gv) {
-      return dec::Launch<T, decltype(gv)::value>::topk(a, t, B, Hkv, D, tokens, s, &handled);
+  auto fused = [&]() {
+    return dispatch_dtype(dtype, [&](auto tv) {
+      using T = decltype(tv);
+      return dispatch_group(G, [&](auto gv) {
+        return dec::Launch<T, decltype(gv)::value>::topk(a, t, B, Hkv, D, tokens, s, &handled);
+      });
     });
-  });
+  };
+  int rc = fused();
   if (rc || handled) return rc;
+  if (t.pair_cnt) {
+    // the pairs do not fit (a group's keys not in LDS): the prescored launch
+    t.pair_cnt = nullptr;
+    rc = topk::criticality_split_scores(q, q_stride_b, q_stride_h, kmin, kmax, s_stride_b,
+                                        s_stride_h, s_stride_page, alibi_slopes, scores, B, H,
+                                        Hkv, D, num_pages, page_size, seq_len, q_pos, nullptr,
+                                        dtype, s, t.scan_rev, t.scan_nt);
+    if (rc) return rc;
+    t.prescored = 1;
+    rc = fused();
+    if (rc || handled) return rc;
+  }
   return two_launches();
 }
 

@@ -73,21 +73,22 @@ def test_topk_step_same_bits_in_both_orders(B, Hkv, G, dtype):
         _equal(got[0][1], table, "page table")
 
 
-@pytest.mark.parametrize("fill", ["random", "ones"])
-def test_paired_topk_any_workspace(fill):
-    """B * Hkv = 128 with single-head groups runs the paired launch (two
+@pytest.mark.parametrize("B,Hkv,G,fill", [(4, 32, 1, "random"), (4, 32, 1, "ones"),
+                                          (8, 16, 2, "random")])
+def test_paired_topk_any_workspace(B, Hkv, G, fill):
+    """B * Hkv = 128 with groups of at most 2 runs the paired launch (two
     workgroups per (b, kv head) scanning half of its pages each); its arrival
     words live in the decode workspace, which a caller need not initialise.
     Random bytes, or every byte 0xff, in the workspace between steps leave
     the results unchanged."""
     from entmaxkv_amd import PagedKVCache, sparse_attention_decode_paged
-    _case(test="paired_workspace", fill=fill)
+    _case(test="paired_workspace", B=B, Hkv=Hkv, G=G, fill=fill)
     dtype = "fp16"
     rng = np.random.default_rng(820)
-    B, Hkv, S, D, budget = 4, 32, 16 * 200 + 9, 128, 1024
+    S, D, budget = 16 * 200 + 9, 128, 1024
     k = randn(rng, (B, Hkv, S, D), dtype)
     v = randn(rng, (B, Hkv, S, D), dtype)
-    q = to_dev(randn(rng, (B, Hkv, 1, D), dtype), dtype)
+    q = to_dev(randn(rng, (B, Hkv * G, 1, D), dtype), dtype)
     cache = PagedKVCache(page_size=16)
     cache.initialize(to_dev(k, dtype), to_dev(v, dtype))
     got = []
@@ -97,7 +98,7 @@ def test_paired_topk_any_workspace(fill):
                 ws.buf.copy_(torch.randint(0, 256, ws.buf.shape, dtype=torch.uint8))
             else:
                 ws.buf.fill_(255)
-        out = torch.zeros(B, Hkv, 1, D, dtype=TORCH_DT[dtype], device="cuda")
+        out = torch.zeros(B, Hkv * G, 1, D, dtype=TORCH_DT[dtype], device="cuda")
         sparse_attention_decode_paged(q, cache, None, None, out, budget, None, None, alpha=1.5,
                                       niter=2, append_cache=False)
         torch.cuda.synchronize()
