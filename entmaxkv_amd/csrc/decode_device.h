@@ -876,13 +876,72 @@ __device__ __forceinline__ void solve_heads(const DecodeArgs& a, int b, int h0, 
   if (real && sp.pos == 0 && sp.lane == 0) sh.s_tau[g] = t;
 }
 
+// Two workgroups per (b, kv head) (the paired Gaussian launch): each scored
+// the tokens [c0, c1) of the head's n into `sc` (LDS, or the head's workspace
+// row).  Each stores them to the workspace with agent-scope stores (written
+// through to the level every XCD reads; a waitcnt completes them) and
+// exchanges the launch's tag into the pair's word: the first to arrive
+// returns false and is done; the second sets the word back to zero, loads its
+// partner's scores with agent-scope loads into `sc` (in the workspace case
+// storing them back with plain stores, so that its later plain loads see
+// them whatever its L2 holds), folds them into the per-wave maxima and
+// returns true to solve tau and gather V for the head.
+template <int G>
+__device__ __forceinline__ bool pair_handoff(const DecodeArgs& a, int b, int h0, int n, int c0,
+                                             int c1, float* sc, int64_t stride,
+                                             const HeadShared& sh, unsigned long long* word,
+                                             unsigned long long tag) {
+  const int tid = threadIdx.x;
+  float* ws = a.ws_scores + ((int64_t)b * a.H + h0) * a.max_tokens;
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    for (int c = c0 + tid; c < c1; c += kHeadThreads)
+      __hip_atomic_store(ws + (int64_t)g * a.max_tokens + c, sc[g * stride + c], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned long long old =
+        __hip_atomic_exchange(word, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == tag) __hip_atomic_store(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh.flag_cnt[0] = old == tag ? 1 : 0;
+  }
+  __syncthreads();
+  if (sh.flag_cnt[0] == 0) return false;
+  const int p0 = c0 == 0 ? c1 : 0, p1 = c0 == 0 ? n : c0;
+  float m[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -1.0e6f;
+    for (int c = p0 + tid; c < p1; c += kHeadThreads) {
+      const float v = __hip_atomic_load(ws + (int64_t)g * a.max_tokens + c, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+      sc[g * stride + c] = v;
+      m[g] = fmaxf(m[g], v);
+    }
+  }
+  if (sh.wmax) {
+    const int lane = tid & 63, wid = tid >> 6;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float w = wave_max(m[g]);
+      if (lane == 0) sh.wmax[g * kWaves + wid] = fmaxf(sh.wmax[g * kWaves + wid], w);
+    }
+  }
+  __syncthreads();
+  return true;
+}
+
 // Phases 1-3 of one (b, kv head); `sc` points to LDS when kStaged (so every
 // score access is a ds_* instruction) and to the workspace otherwise.
 template <typename T, int LPR, int G, int U, bool kStaged, bool kTableInLds = false>
-__device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int kvh, int n,
+__device__ __forceinline__ bool decode_head_body(const DecodeArgs& a, int b, int kvh, int n,
                                                  float* sc, int64_t stride,
                                                  const HeadShared& sh_in,
-                                                 bool first_chunk_staged = false) {
+                                                 bool first_chunk_staged = false,
+                                                 unsigned long long* pair_word = nullptr,
+                                                 unsigned long long pair_tag = 0,
+                                                 int pair_half = 0) {
   // the per-wave maxima reach the tau solve only when phase 1 runs here
   HeadShared sh = sh_in;
   if (a.scores_ready && !kTableInLds) sh.wmax = nullptr;
@@ -900,12 +959,22 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
   float rmax[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) rmax[g] = -1.0e6f;
+  // paired: this workgroup scores the first or the second half of the tokens
+  // (split on a multiple of 64 tokens, and of 64 pages when the page table is
+  // staged chunk by chunk)
+  int pc0 = 0, pc1 = n;
+  if (pair_word) {
+    const int q = kTableInLds ? 64 : 64 * ps;
+    const int mid = min(n, (n / 2 + q - 1) / q * q);
+    if (pair_half) pc0 = mid;
+    else pc1 = mid;
+  }
   if (kTableInLds) {
     // the whole page table is already in sh.s_pages (written by this workgroup)
-    score_rows<T, LPR, G, kHeadThreads, U>(a, b, kvh, 0, n, sc, stride, sh.s_pages, 0, rmax);
+    score_rows<T, LPR, G, kHeadThreads, U>(a, b, kvh, pc0, pc1, sc, stride, sh.s_pages, 0, rmax);
   } else if (!a.scores_ready) {
-    for (int cb = 0; cb < n; cb += kTablePages * ps) {
-      const int ce = min(n, cb + kTablePages * ps);
+    for (int cb = pc0; cb < pc1; cb += kTablePages * ps) {
+      const int ce = min(pc1, cb + kTablePages * ps);
       const int np = (ce - cb + ps - 1) / ps;
       if (!(first_chunk_staged && cb == 0)) {
         for (int i = tid; i < np; i += kHeadThreads) sh.s_pages[i] = pi[cb / ps + i];
@@ -925,6 +994,8 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
   }
   EKV_WSTAMP(5);
   __syncthreads();
+  if (pair_word && !pair_handoff<G>(a, b, h0, n, pc0, pc1, sc, stride, sh, pair_word, pair_tag))
+    return false;
   EKV_STAMP(3);
 
   // phase 2: tau per head, one team of waves per head: for lists up to 4096
@@ -1085,6 +1156,7 @@ __device__ __forceinline__ void decode_head_body(const DecodeArgs& a, int b, int
     }
     __syncthreads();
   }
+  return true;
 }
 
 template <typename T, int LPR, int G, int U>
@@ -1355,14 +1427,22 @@ struct GaussArgs {
   float n_tokens, log_n_factor;
   int tau_iters;
   float tol;
+  // the paired launch (groups of 4 and 8 at most half the CU count): two
+  // workgroups per (b, kv head) share the K scoring of selections of at least
+  // kPairMinTokens tokens (below that the second leaves after the
+  // selection); one arrival word per pair (see pair_handoff)
+  unsigned long long* pair_cnt = nullptr;
+  unsigned long long pair_tag = 0;
 };
+
+constexpr int kPairMinTokens = 8192;
 
 // One (b, kv head) per workgroup end to end: the global moments of every head
 // (for the batch-wide mean sigma_g of the automatic margins) and of its own G
 // heads, their tau-hat (one wave per head), threshold selection + pack +
 // clamp, then phases 1-3 of the decode on the selected pages starting from
 // the clamped tau (given-tau mode) or solving it (exact mode).
-template <typename T, int LPR, int G, int UD>
+template <typename T, int LPR, int G, int UD, bool kPair = false>
 __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArgs a, GaussArgs f) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int D = LPR * VEC;
@@ -1384,7 +1464,8 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
   sh.wmax = wmax;
 
   const int tid = threadIdx.x, wid = tid >> 6;
-  const int bkv = blockIdx.x;
+  const int bkv = kPair ? blockIdx.x >> 1 : blockIdx.x;
+  const int pair_half = kPair ? blockIdx.x & 1 : 0;
   const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
   const gauss::SelectArgs& sel = f.sel;
   EKV_STAMP(0);
@@ -1487,15 +1568,26 @@ __global__ __launch_bounds__(kHeadThreads) void gaussian_decode_kernel(DecodeArg
                                : sel.last_page_size;
   int n = count > 0 ? (count - 1) * sel.page_size + lps : 0;
   n = min(n, min(count * sel.page_size, a.max_tokens));
+  // paired: both workgroups selected the same pages (and stored the same
+  // outputs); they share the scoring of large selections, and the second
+  // leaves at once for small ones
+  unsigned long long* word = nullptr;
+  if constexpr (kPair) {
+    if (n < kPairMinTokens && pair_half) return;
+    if (n >= kPairMinTokens) word = f.pair_cnt + bkv;
+  }
   // the first kTablePages page ids are already in s_pages (all of them when
   // count <= kTablePages: the decode then reads no page id from global memory)
   if (n <= a.stage_cap && count <= kTablePages) {
-    decode_head_body<T, LPR, G, UD, true, true>(a, b, kvh, n, stage, a.stage_cap, sh);
+    decode_head_body<T, LPR, G, UD, true, true>(a, b, kvh, n, stage, a.stage_cap, sh, false,
+                                                word, f.pair_tag, pair_half);
   } else if (n <= a.stage_cap) {
-    decode_head_body<T, LPR, G, UD, true>(a, b, kvh, n, stage, a.stage_cap, sh, true);
+    decode_head_body<T, LPR, G, UD, true>(a, b, kvh, n, stage, a.stage_cap, sh, true, word,
+                                          f.pair_tag, pair_half);
   } else {
     float* ws = a.ws_scores + ((int64_t)b * a.H + kvh * G) * a.max_tokens;
-    decode_head_body<T, LPR, G, UD, false>(a, b, kvh, n, ws, a.max_tokens, sh, true);
+    decode_head_body<T, LPR, G, UD, false>(a, b, kvh, n, ws, a.max_tokens, sh, true, word,
+                                           f.pair_tag, pair_half);
   }
 }
 

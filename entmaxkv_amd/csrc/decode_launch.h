@@ -114,7 +114,8 @@ int Launch<T, G>::gaussian(DecodeArgs a, GaussArgs f, int B, int Hkv, int D, int
   return dispatch_lpr<T>(D, [&](auto lpr) {
     constexpr int LPR = decltype(lpr)::value;
     constexpr int UD = G >= 4 ? 2 : 8 / G;
-    auto kern = gaussian_decode_kernel<T, LPR, G, UD>;
+    auto kern = f.pair_cnt ? gaussian_decode_kernel<T, LPR, G, UD, true>
+                           : gaussian_decode_kernel<T, LPR, G, UD>;
     // scores stay in LDS up to what the static LDS leaves (else the workspace)
     const int64_t avail = lds_left((const void*)kern, "gaussian_decode_kernel");
     if (avail < 0) return EKV_ERR_HIP;
@@ -124,7 +125,8 @@ int Launch<T, G>::gaussian(DecodeArgs a, GaussArgs f, int B, int Hkv, int D, int
     const size_t lds = (size_t)cap * G * sizeof(float);
     const int rc = set_dynamic_lds((const void*)kern, lds, "gaussian_decode_kernel");
     if (rc) return rc;
-    hipLaunchKernelGGL(kern, dim3(B * Hkv), dim3(kHeadThreads), lds, s, a, f);
+    hipLaunchKernelGGL(kern, dim3(B * Hkv * (f.pair_cnt ? 2 : 1)), dim3(kHeadThreads), lds, s,
+                       a, f);
     return check_launch("gaussian_decode_kernel");
   });
 }

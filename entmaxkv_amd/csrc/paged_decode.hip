@@ -107,7 +107,9 @@ extern "C" int64_t ekv_decode_workspace_bytes(int B, int H, int Hkv, int D, int 
   (void)Hkv;
   (void)D;
   (void)splits;
-  return ((int64_t)B * H * max_tokens * 4 + 255) / 256 * 256;
+  // fp32 scores [B, H, max_tokens], then the paired Gaussian launch's words
+  return ((int64_t)B * H * max_tokens * 4 + 255) / 256 * 256 +
+         ((int64_t)B * H * 8 + 255) / 256 * 256;
 }
 
 // The decode launch(es); force_split spreads every head over many workgroups
@@ -489,6 +491,16 @@ extern "C" int ekv_gaussian_paged_entmax_decode(
   f.log_n_factor = (float)sqrt(2.0 * log((double)n_tokens + 1.0));
   f.tau_iters = tau_iters;
   f.tol = tol;
+  if (G >= 4 && 2 * B * Hkv <= device_cus()) {
+    // two workgroups per (b, kv head) share large selections' K scoring; the
+    // arrival words follow the workspace's scores (a fresh tag per call, as
+    // in the paired top-k launch)
+    static std::atomic<unsigned long long> launches{0};
+    f.pair_cnt = (unsigned long long*)((char*)workspace +
+                                       ((int64_t)B * H * max_tokens * 4 + 255) / 256 * 256);
+    f.pair_tag = ((launches.fetch_add(1, std::memory_order_relaxed) + 1) *
+                  0xD1B54A32D192ED03ull) | 1ull;
+  }
   return dispatch_dtype(dtype, [&](auto tv) {
     using T = decltype(tv);
     return dispatch_group(G, [&](auto gv) {

@@ -843,6 +843,33 @@ def test_gaussian_fused_step(dtype, G, tau_mode, alpha, B, Hkv, D, keys):
     _check_gaussian_step(cache, q, k, v, out, dtype, G, tau_mode, alpha, [S] * B)
 
 
+@pytest.mark.parametrize("tau_mode", ["corrected", "exact"])
+def test_gaussian_paired_decode(tau_mode):
+    """Groups of 4 at B * Hkv = 128 run the paired Gaussian launch: two
+    workgroups per (b, kv head) select the same pages, and from 8192 selected
+    tokens on each scores half of them and the later one, after a hand-off of
+    its partner's scores, solves tau and gathers V.  N(0, 1) keys select about
+    57 % of 1024 pages here (about 9300 tokens), so the hand-off runs; the
+    step is checked against the oracle like any other."""
+    from entmaxkv_amd import PagedKVCache, sparse_attention_decode_gaussian_aware_entmax
+    dtype, G, alpha, B, Hkv, D = "bf16", 4, 2.0, 16, 8, 64
+    _case(test="gaussian_paired", tau_mode=tau_mode, B=B, Hkv=Hkv, G=G, D=D)
+    rng = np.random.default_rng(640)
+    S, ps = 16 * 1024 + 5, 16
+    H = Hkv * G
+    q, k, v = (randn(rng, (B, H, 1, D), dtype), randn(rng, (B, Hkv, S, D), dtype),
+               randn(rng, (B, Hkv, S, D), dtype))
+    cache = PagedKVCache(page_size=ps)
+    cache.initialize(to_dev(k, dtype), to_dev(v, dtype))
+    out = torch.zeros(B, H, 1, D, dtype=TORCH_DT[dtype], device="cuda")
+    sparse_attention_decode_gaussian_aware_entmax(to_dev(q, dtype), cache, None, None, out,
+                                                  alpha=alpha, tau_mode=tau_mode)
+    torch.cuda.synchronize()
+    sel = cache.last_num_selected_per_head
+    assert int(sel.min()) * ps >= 8192, "the selection is too small to take the hand-off"
+    _check_gaussian_step(cache, q, k, v, out, dtype, G, tau_mode, alpha, [S] * B)
+
+
 @pytest.mark.parametrize("path", ["head", "split"])
 def test_gaussian_alibi_step(path):
     """ALiBi through the Gaussian step: page-mean bias on the page means,
