@@ -65,7 +65,7 @@ extern "C" int ekv_topk_paged_entmax_decode_noalloc(
   const int64_t need = ekv_decode_workspace_bytes(B, H, Hkv, D, splits, max_tokens);
   EKV_REQUIRE(need <= kScratchBytes,
               "ekv_topk_paged_entmax_decode_noalloc: the step needs %lld workspace bytes "
-              "(B * H * max_tokens * 4), more than the %lld of the static scratch; use "
+              "(ekv_decode_workspace_bytes), more than the %lld of the static scratch; use "
               "ekv_topk_paged_entmax_decode with a caller workspace",
               (long long)need, (long long)kScratchBytes);
   void* ws = nullptr;

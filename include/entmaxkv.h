@@ -84,7 +84,9 @@ int ekv_topk_pages(const void* scores, int B, int H, int Hkv, int num_pages, int
                    int32_t* page_indices, int64_t pi_stride_b, int64_t pi_stride_h, int dtype,
                    void* stream);
 
-/* Workspace for ekv_paged_entmax_decode. */
+/* Workspace for ekv_paged_entmax_decode, ekv_topk_paged_entmax_decode and
+ * ekv_gaussian_paged_entmax_decode: fp32 score rows, then one 8-byte word
+ * per (b, head) for the paired launches.  Any contents on entry. */
 int64_t ekv_decode_workspace_bytes(int B, int H, int Hkv, int D, int splits, int max_tokens);
 
 /* Paged alpha-entmax decode over the compacted page table (keyed by kv head).
@@ -172,8 +174,8 @@ int ekv_append_topk_paged_entmax_decode(
  * allocate device memory (code under hipGraph capture, serving loops that
  * forbid hipMalloc).  The workspace is a static device array of
  * EKV_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a step
- * whose workspace (ekv_decode_workspace_bytes: B * H * max_tokens * 4 bytes)
- * exceeds it is rejected with EKV_ERR_ARG and nothing is launched.  Every
+ * whose workspace (ekv_decode_workspace_bytes: B * H * max_tokens * 4 bytes
+ * of scores plus B * H * 8 bytes of pair words, each rounded up to 256) exceeds it is rejected with EKV_ERR_ARG and nothing is launched.  Every
  * call on one GPU shares that GPU's array, so calls that overlap on one GPU
  * (other streams, other host threads) race and must be serialised by the
  * caller.  Results equal ekv_topk_paged_entmax_decode's. */
